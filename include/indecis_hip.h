@@ -1,0 +1,175 @@
+/*
+ * indecis_hip.h — C ABI of the MI355X (gfx950) int8 ModernBERT encoder.
+ *
+ * This is the drop-in boundary for indecis's int8 encoder forward pass:
+ * the body of internal/modernbert.(*Model).run (infer.go:304-430) and the
+ * linalg entry points it calls. A cgo file built under the `rocm` tag
+ * binds these functions; EncodeSeqs, EncodeTokens and
+ * Encode keep their Go signatures, so model.go:425, batch.go:71,
+ * spans.go:423, distill.go:121 and open.go:131 switch with no change.
+ *
+ * Conventions: plain pointers and sizes, no GPU types in signatures. Host
+ * pointers are borrowed for the call only. Every function returns 0 on
+ * success or a nonzero IXH_E* code; ixh_last_error() then gives the
+ * message of the calling thread's last failure, worded as the reference
+ * words its errors where it has one ("modernbert: id 5 out of
+ * vocabulary"). Model handles are safe to share between threads once
+ * their weights are set: each call takes its own stream and workspace
+ * from a pool (the reference's workspaces, infer.go:229-235,342-346).
+ */
+#ifndef INDECIS_HIP_H
+#define INDECIS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  IXH_OK = 0,
+  IXH_EINVAL = 1,   /* bad argument (the reference panics or errors) */
+  IXH_ERANGE = 2,   /* id out of vocabulary (infer.go:310-312) */
+  IXH_ESTATE = 3,   /* weights missing (infer.go:170-182) */
+  IXH_EHIP = 4,     /* HIP runtime error ("modernbert: hip: ...") */
+  IXH_ENOMEM = 5,
+};
+
+/* modernbert.Config (internal/modernbert/model.go:26-49) plus the Go simd
+ * vector width of the host whose results are reproduced. */
+typedef struct ixh_config {
+  int hidden;          /* hidden_size */
+  int layers;          /* num_hidden_layers */
+  int heads;           /* num_attention_heads (head dim must be 64) */
+  int intermediate;    /* intermediate_size */
+  int vocab;           /* vocab_size */
+  double norm_eps;     /* norm_eps */
+  int global_every;    /* global_attn_every_n_layers (IsGlobal: l%n == 0) */
+  int local_attention; /* local_attention; window = local_attention/2 */
+  double global_theta; /* global_rope_theta */
+  double local_theta;  /* local_rope_theta */
+  int pooling;         /* IXH_POOL_MEAN or IXH_POOL_CLS (Config.CLS) */
+  int lanes;           /* Go simd V: 0 (no simd build), 4, 8 or 16 */
+} ixh_config;
+
+enum { IXH_POOL_MEAN = 0, IXH_POOL_CLS = 1 };
+enum { IXH_MAT_QKV = 0, IXH_MAT_O = 1, IXH_MAT_I = 2, IXH_MAT_OMLP = 3 };
+enum { IXH_NORM_EMB = 0, IXH_NORM_ATTN = 1, IXH_NORM_MLP = 2, IXH_NORM_FINAL = 3 };
+/* Weight layouts: rows = q[n][k] (row j is output channel j, the
+ * transformers [out, in] layout PackB8 reads with transB); panels = the
+ * PackedB8.data order p*kq*64 + q*64 + c*4 + t (linalg/int8.go:30). */
+enum { IXH_LAYOUT_ROWS = 0, IXH_LAYOUT_PANELS = 1 };
+enum { IXH_OUT_POOLED = 0, IXH_OUT_TOKENS = 1 };
+
+typedef struct ixh_model ixh_model;
+typedef struct ixh_packed_b8 ixh_packed_b8;
+
+/* Message of this thread's last failure ("" if none). */
+const char *ixh_last_error(void);
+
+/* Number of visible GPUs. */
+int ixh_device_count(int *count);
+
+/* ---- model (internal/modernbert) -------------------------------------- */
+
+/* Replaces modernbert.FromTensors + packs() (model.go:181-234,
+ * infer.go:184-219) for the int8 path: creates an empty model on device;
+ * the set_* calls upload what PackB8 and the tensors hold. */
+int ixh_model_create(const ixh_config *cfg, int device, ixh_model **out);
+void ixh_model_destroy(ixh_model *m);
+
+/* One packed int8 matrix of a layer (packedLayer, infer.go:84-87,
+ * 209-216): q int8 and the per-output-channel scale of PackedB8
+ * (int8.go:27-34); colsum is derived from q. Shapes: QKV [3H][H], O [H][H],
+ * I [2I][H] (GELU input rows then gate rows, model.go:96), OMLP [H][I]. */
+int ixh_model_set_matrix(ixh_model *m, int layer, int which, const int8_t *q,
+                         const float *scale, int layout);
+
+/* LayerNorm weights (no bias): EMB and FINAL ignore layer; ATTN of layer 0
+ * does not exist (model.go:92) and is rejected. */
+int ixh_model_set_norm(ixh_model *m, int which, int layer, const float *gamma);
+
+/* Embedding table (embRow infer.go:52-59, mappedEmbeddings.Row
+ * embeddings.go:48-68): float32 [V][H]; or bf16 [V][H] with n_exact float32
+ * rows overriding ids exact_ids; or int8 [V][H] with one scale per row. */
+int ixh_model_set_embeddings_f32(ixh_model *m, const float *table);
+int ixh_model_set_embeddings_bf16(ixh_model *m, const uint16_t *table,
+                                  const int32_t *exact_ids,
+                                  const float *exact_rows, int n_exact);
+int ixh_model_set_embeddings_i8(ixh_model *m, const int8_t *table,
+                                const float *row_scale);
+
+/* Optional: RoPE tables as Go's ropeFor computes them (model.go:256-277),
+ * cos/sin [rows][head_dim/2], for the global (is_global=1) or local theta.
+ * Without them the library computes the same formula with the C library's
+ * pow/cos/sin. */
+int ixh_model_set_rope(ixh_model *m, int is_global, const float *cos_t,
+                       const float *sin_t, int rows);
+
+/* Drops the uploaded weights (Invalidate/SetInt8, infer.go:95-135): the
+ * next encode fails with IXH_ESTATE until they are set again. */
+int ixh_model_invalidate(ixh_model *m);
+
+/* EncodeSeqs (infer.go:261-289): ids of B sequences laid end to end,
+ * offs[B+1] cumulative (offs[0] = 0), out [B][H] pooled (mean or CLS). */
+int ixh_encode_seqs(ixh_model *m, const int32_t *ids, const int32_t *offs,
+                    int B, float *out);
+/* EncodeTokens (infer.go:293-299): out [offs[B]][H] final states. */
+int ixh_encode_tokens(ixh_model *m, const int32_t *ids, const int32_t *offs,
+                      int B, float *out);
+/* Either of the above (out_kind IXH_OUT_POOLED or IXH_OUT_TOKENS) with ids
+ * and out already in device memory of the model's GPU (offs stays on the
+ * host), on `stream` (a hipStream_t, or NULL for the workspace's own
+ * stream). Ids are checked on the device. Returns when the work is done. */
+int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs,
+                      int B, int out_kind, float *d_out, void *stream);
+
+/* head.logits (heads.go:63-74) on host rows: z[t][r] = sum_i
+ * f64(w[r][i]) f64(x[t][i]) + f64(b[r]), computed on the model's GPU. */
+int ixh_head_logits(ixh_model *m, const float *x, int T, const float *w,
+                    const float *b, int rows, double *z);
+
+/* ---- linalg ------------------------------------------------------------- */
+
+/* A PackedB8 on device (linalg/int8.go:27-77): k x n, from q and scale as
+ * for ixh_model_set_matrix. */
+int ixh_packb8_create(int device, const int8_t *q, const float *scale, int k,
+                      int n, int layout, ixh_packed_b8 **out);
+void ixh_packb8_destroy(ixh_packed_b8 *b);
+
+/* MatMul8N (linalg/int8.go:89-155): c[m][n] (+)= a[m][k] . B, a quantised
+ * per row as quantizeA does. Host buffers. */
+int ixh_matmul8(ixh_packed_b8 *b, float *c, const float *a, int m,
+                int accumulate);
+
+/* The integers MatMul8N works with, for bit-exact checks: the quantised
+ * activations (signed, i.e. the reference's uint8 minus 128) aq[m][k],
+ * their scales sa[m], and the reference tile (microKernel8Go,
+ * int8.go:214-227) tile[m][n] = sum (aq+128)*q. */
+int ixh_matmul8_tile(ixh_packed_b8 *b, const float *a, int m, int8_t *aq,
+                     float *sa, int32_t *tile);
+
+/* LayerNormRow (linalg/vec_simd.go:285-327) of m rows of h values, then,
+ * if q is not NULL, quantizeA of the result (q[m][h] signed, sa[m]) — the
+ * fused LN + quantisation of the encoder. out may be NULL. */
+int ixh_layernorm_quant(int device, const float *x, int m, int h,
+                        const float *gamma, double eps, int lanes, float *out,
+                        int8_t *q, float *sa);
+
+/* LN + quantizeA + MatMul8N + GeluMul (infer.go:404-418): the fused Wi
+ * step. g[m][n/2] = gelu(z[:, :n/2]) * z[:, n/2:] with z = LN(x) . B
+ * (B is k x n, n/2 a multiple of 32); also the int32 tile if not NULL. */
+int ixh_ln_matmul8_geglu(ixh_packed_b8 *b, const float *x, int m,
+                         const float *gamma, double eps, int lanes, float *g,
+                         int32_t *tile);
+
+/* Attend8 (linalg/attention8.go:70-73): o[n][64] = attention of q over k, v
+ * (n x 64 each), window < 0 global, scores scaled by scale. */
+int ixh_attend8(int device, float *o, const float *q, const float *k,
+                const float *v, int n, int d, int window, float scale,
+                int lanes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

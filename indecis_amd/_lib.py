@@ -1,0 +1,107 @@
+"""ctypes binding of libindecis_hip.so (include/indecis_hip.h).
+
+The library is built in-tree by indecis_amd.build (or __graft_entry__.build)
+and loaded from indecis_amd/libindecis_hip.so. There is no fallback: if it
+is missing, or no GPU is visible when a GPU entry point is called, these
+functions raise.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SO_PATH = os.path.join(HERE, "libindecis_hip.so")
+
+# every exported entry point, as declared in include/indecis_hip.h
+EXPORTS = [
+    "ixh_last_error", "ixh_device_count", "ixh_model_create", "ixh_model_destroy",
+    "ixh_model_set_matrix", "ixh_model_set_norm", "ixh_model_set_embeddings_f32",
+    "ixh_model_set_embeddings_bf16", "ixh_model_set_embeddings_i8", "ixh_model_set_rope",
+    "ixh_model_invalidate", "ixh_encode_seqs", "ixh_encode_tokens", "ixh_encode_device",
+    "ixh_head_logits", "ixh_packb8_create", "ixh_packb8_destroy", "ixh_matmul8",
+    "ixh_matmul8_tile", "ixh_layernorm_quant", "ixh_ln_matmul8_geglu", "ixh_attend8",
+]
+
+IXH_OK, IXH_EINVAL, IXH_ERANGE, IXH_ESTATE, IXH_EHIP, IXH_ENOMEM = range(6)
+POOL_MEAN, POOL_CLS = 0, 1
+MAT_QKV, MAT_O, MAT_I, MAT_OMLP = range(4)
+NORM_EMB, NORM_ATTN, NORM_MLP, NORM_FINAL = range(4)
+LAYOUT_ROWS, LAYOUT_PANELS = 0, 1
+OUT_POOLED, OUT_TOKENS = 0, 1
+
+
+class IxhError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+class IxhConfig(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_int), ("layers", C.c_int), ("heads", C.c_int),
+        ("intermediate", C.c_int), ("vocab", C.c_int), ("norm_eps", C.c_double),
+        ("global_every", C.c_int), ("local_attention", C.c_int),
+        ("global_theta", C.c_double), ("local_theta", C.c_double),
+        ("pooling", C.c_int), ("lanes", C.c_int),
+    ]
+
+
+_lib = None
+vp = C.c_void_p
+
+
+def lib():
+    """Loads the library (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(SO_PATH):
+        raise RuntimeError(
+            f"indecis_amd: {SO_PATH} is missing; run __graft_entry__.build() "
+            "(the HIP path has no CPU fallback)")
+    L = C.CDLL(SO_PATH)
+    L.ixh_last_error.restype = C.c_char_p
+    L.ixh_last_error.argtypes = []
+    sig = {
+        "ixh_device_count": [C.POINTER(C.c_int)],
+        "ixh_model_create": [C.POINTER(IxhConfig), C.c_int, C.POINTER(vp)],
+        "ixh_model_set_matrix": [vp, C.c_int, C.c_int, vp, vp, C.c_int],
+        "ixh_model_set_norm": [vp, C.c_int, C.c_int, vp],
+        "ixh_model_set_embeddings_f32": [vp, vp],
+        "ixh_model_set_embeddings_bf16": [vp, vp, vp, vp, C.c_int],
+        "ixh_model_set_embeddings_i8": [vp, vp, vp],
+        "ixh_model_set_rope": [vp, C.c_int, vp, vp, C.c_int],
+        "ixh_model_invalidate": [vp],
+        "ixh_encode_seqs": [vp, vp, vp, C.c_int, vp],
+        "ixh_encode_tokens": [vp, vp, vp, C.c_int, vp],
+        "ixh_encode_device": [vp, vp, vp, C.c_int, C.c_int, vp, vp],
+        "ixh_head_logits": [vp, vp, C.c_int, vp, vp, C.c_int, vp],
+        "ixh_packb8_create": [C.c_int, vp, vp, C.c_int, C.c_int, C.c_int, C.POINTER(vp)],
+        "ixh_matmul8": [vp, vp, vp, C.c_int, C.c_int],
+        "ixh_matmul8_tile": [vp, vp, C.c_int, vp, vp, vp],
+        "ixh_layernorm_quant": [C.c_int, vp, C.c_int, C.c_int, vp, C.c_double, C.c_int, vp, vp, vp],
+        "ixh_ln_matmul8_geglu": [vp, vp, C.c_int, vp, C.c_double, C.c_int, vp, vp],
+        "ixh_attend8": [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int],
+    }
+    for name, args in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = C.c_int
+    L.ixh_model_destroy.argtypes = [vp]
+    L.ixh_model_destroy.restype = None
+    L.ixh_packb8_destroy.argtypes = [vp]
+    L.ixh_packb8_destroy.restype = None
+    _lib = L
+    return L
+
+
+def check(rc):
+    """Raises IxhError with the library's message for a nonzero code."""
+    if rc != IXH_OK:
+        msg = lib().ixh_last_error().decode(errors="replace")
+        raise IxhError(rc, msg)
+
+
+def device_count():
+    n = C.c_int(0)
+    check(lib().ixh_device_count(C.byref(n)))
+    return n.value

@@ -1,0 +1,1142 @@
+// ixh_api.cpp — the C ABI of include/indecis_hip.h: model state on the
+// GPU, a pool of (stream, workspace) pairs, and the encoder forward pass of
+// internal/modernbert.(*Model).run (infer.go:304-430) as a sequence of
+// gfx950 kernels on one stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/indecis_hip.h"
+#include "ixh_internal.h"
+
+using namespace ixh;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIPCK(call)                                                                      \
+  do {                                                                                   \
+    hipError_t e_ = (call);                                                              \
+    if (e_ != hipSuccess)                                                                \
+      return fail(IXH_EHIP, "modernbert: hip: %s (%s)", hipGetErrorString(e_), #call);   \
+  } while (0)
+#define LAUNCHCK(what)                                                                   \
+  do {                                                                                   \
+    hipError_t e_ = hipGetLastError();                                                   \
+    if (e_ != hipSuccess)                                                                \
+      return fail(IXH_EHIP, "modernbert: hip: %s (launch %s)", hipGetErrorString(e_), what); \
+  } while (0)
+
+inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+// Device buffer that grows and never shrinks.
+struct DevBuf {
+  void *p = nullptr;
+  size_t n = 0;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  int ensure(size_t bytes) {
+    if (bytes <= n) return IXH_OK;
+    if (p) HIPCK(hipFree(p));
+    p = nullptr;
+    n = 0;
+    size_t want = round_up(std::max<size_t>(bytes, 256), 256);
+    HIPCK(hipMalloc(&p, want));
+    n = want;
+    return IXH_OK;
+  }
+  template <class T> T *as() const { return (T *)p; }
+};
+
+struct PinBuf {
+  void *p = nullptr;
+  size_t n = 0;
+  ~PinBuf() {
+    if (p) (void)hipHostFree(p);
+  }
+  int ensure(size_t bytes) {
+    if (bytes <= n) return IXH_OK;
+    if (p) HIPCK(hipHostFree(p));
+    p = nullptr;
+    n = 0;
+    size_t want = round_up(std::max<size_t>(bytes, 4096), 4096);
+    HIPCK(hipHostMalloc(&p, want, hipHostMallocDefault));
+    n = want;
+    return IXH_OK;
+  }
+};
+
+struct DeviceGuard {
+  int prev = -1;
+  hipError_t err = hipSuccess;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    err = hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+#define DEVGUARD(dev)                                                                    \
+  DeviceGuard dg_(dev);                                                                  \
+  if (dg_.err != hipSuccess)                                                             \
+    return fail(IXH_EHIP, "modernbert: hip: %s (hipSetDevice %d)", hipGetErrorString(dg_.err), dev);
+
+// A quantised weight matrix on the device, padded to the GEMM tiles:
+// rows to a multiple of 128 (zero channels), depth to a multiple of 64.
+struct Mat {
+  int k = 0, n = 0, kp = 0, np = 0;
+  bool set = false;
+  DevBuf q, sb, zc, c128;
+};
+
+// Rows [n][k] from either layout.
+std::vector<int8_t> to_rows(const int8_t *q, int k, int n, int layout) {
+  std::vector<int8_t> rows((size_t)n * k);
+  if (layout == IXH_LAYOUT_ROWS) {
+    memcpy(rows.data(), q, rows.size());
+    return rows;
+  }
+  const int kq = (k + 3) / 4;
+  for (int j = 0; j < n; j++)
+    for (int t = 0; t < k; t++)
+      rows[(size_t)j * k + t] = q[(size_t)(j / 16) * kq * 64 + (t / 4) * 64 + (j % 16) * 4 + t % 4];
+  return rows;
+}
+
+// Uploads rows [n][k] + scales; perm (optional) gives the source row of
+// each destination row (the GeGLU interleave).
+int upload_mat(Mat &M, const std::vector<int8_t> &rows, const float *scale, int k, int n,
+               const std::vector<int> *perm) {
+  M.k = k;
+  M.n = n;
+  M.kp = (int)round_up(k, 64);
+  M.np = (int)round_up(n, 128);
+  std::vector<int8_t> q((size_t)M.np * M.kp, 0);
+  std::vector<float> sb(M.np, 0.f), zc(M.np, 0.f);
+  std::vector<int32_t> c128(M.np, 0);
+  for (int d = 0; d < n; d++) {
+    const int s = perm ? (*perm)[d] : d;
+    int32_t colsum = 0;
+    for (int t = 0; t < k; t++) {
+      const int8_t v = rows[(size_t)s * k + t];
+      q[(size_t)d * M.kp + t] = v;
+      colsum += v;
+    }
+    sb[d] = scale[s];
+    // PackB8: zc = 128*float32(colsum) (int8.go:72-75)
+    zc[d] = 128.0f * (float)colsum;
+    c128[d] = 128 * colsum;
+  }
+  int rc;
+  if ((rc = M.q.ensure(q.size())) || (rc = M.sb.ensure(sb.size() * 4)) ||
+      (rc = M.zc.ensure(zc.size() * 4)) || (rc = M.c128.ensure(c128.size() * 4)))
+    return rc;
+  HIPCK(hipMemcpy(M.q.p, q.data(), q.size(), hipMemcpyHostToDevice));
+  HIPCK(hipMemcpy(M.sb.p, sb.data(), sb.size() * 4, hipMemcpyHostToDevice));
+  HIPCK(hipMemcpy(M.zc.p, zc.data(), zc.size() * 4, hipMemcpyHostToDevice));
+  HIPCK(hipMemcpy(M.c128.p, c128.data(), c128.size() * 4, hipMemcpyHostToDevice));
+  M.set = true;
+  return IXH_OK;
+}
+
+// Interleave of the Wi rows for the GeGLU epilogue: destination chunk c of
+// 64 rows = GELU-input rows 32c..32c+31, then gate rows I+32c..I+32c+31.
+std::vector<int> geglu_perm(int I) {
+  std::vector<int> p(2 * I);
+  for (int d = 0; d < 2 * I; d++) {
+    const int c = d / 64, w = d % 64;
+    p[d] = w < 32 ? 32 * c + w : I + 32 * c + (w - 32);
+  }
+  return p;
+}
+
+// The GeGLU columns computed with the fused-multiply-add GELU: the AVX2
+// prefix (multiple of 16) then whole SIMD vectors (vec_simd.go:138-156).
+int gelu_fma_cols(int I, int lanes) {
+  int i = I & ~15;
+  if (lanes > 0)
+    while (i + lanes <= I) i += lanes;
+  return i;
+}
+
+// ropeFor (model.go:256-277): inv = f32(1/theta^(2i/D)), angle =
+// f64(f32(p)*inv), cos/sin in float64 rounded to float32.
+void rope_table(double theta, int D, int rows, std::vector<float> &c, std::vector<float> &s) {
+  const int half = D / 2;
+  c.assign((size_t)rows * half, 0.f);
+  s.assign((size_t)rows * half, 0.f);
+  for (int i = 0; i < half; i++) {
+    const float inv = (float)(1.0 / std::pow(theta, (double)(2 * i) / (double)D));
+    for (int p = 0; p < rows; p++) {
+      const double f = (double)((float)p * inv);
+      c[(size_t)p * half + i] = (float)std::cos(f);
+      s[(size_t)p * half + i] = (float)std::sin(f);
+    }
+  }
+}
+
+struct RopeTab {
+  int rows = 0;
+  bool user = false;
+  std::shared_ptr<DevBuf> cos_t, sin_t;
+};
+
+struct Workspace {
+  hipStream_t stream = nullptr;
+  DevBuf ids, offs, padoff, pos, blocks, x, xn, qkv, xq, sa, qq, sq, kp, ks, vt, vs, ctx, g,
+      pooled, flag;
+  PinBuf host;
+  ~Workspace() {
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+}  // namespace
+
+struct ixh_model {
+  ixh_config cfg{};
+  int device = 0;
+  int D = 64;
+  struct Layer {
+    Mat qkv, o, i, omlp;
+    DevBuf attn_norm, mlp_norm;
+    bool attn_norm_set = false, mlp_norm_set = false;
+  };
+  std::vector<Layer> layers;
+  DevBuf emb_norm, final_norm;
+  bool emb_norm_set = false, final_norm_set = false;
+  int emb_format = -1;
+  DevBuf emb_table, emb_exact_slot, emb_exact_rows, emb_i8_scale;
+  std::mutex rope_mu;
+  RopeTab rope[2];  // 0 local, 1 global
+  std::vector<std::shared_ptr<DevBuf>> rope_graveyard;
+  std::mutex pool_mu;
+  std::vector<Workspace *> pool;
+  std::atomic<bool> weights_valid{true};
+  ~ixh_model() {
+    for (Workspace *w : pool) delete w;
+  }
+};
+
+struct ixh_packed_b8 {
+  int device = 0;
+  Mat mat;
+  std::vector<int8_t> rows;  // host copy, for the GeGLU interleave
+  std::vector<float> scale;
+  std::mutex mu;
+  Mat geglu;
+  bool geglu_set = false;
+};
+
+namespace {
+
+int validate_config(const ixh_config &c) {
+  if (c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.intermediate <= 0 || c.vocab <= 0)
+    return fail(IXH_EINVAL, "modernbert: invalid dimensions");
+  if (c.hidden % c.heads != 0 || (c.hidden / c.heads) % 2 != 0)
+    return fail(IXH_EINVAL, "modernbert: hidden_size %d incompatible with %d heads", c.hidden,
+                c.heads);
+  if (c.global_every <= 0 || c.local_attention <= 0)
+    return fail(IXH_EINVAL, "modernbert: invalid attention windows");
+  if (c.hidden / c.heads != 64)
+    return fail(IXH_EINVAL, "modernbert: hip: head dimension %d not supported (64)",
+                c.hidden / c.heads);
+  if (c.hidden % 64 != 0 || c.intermediate % 32 != 0)
+    return fail(IXH_EINVAL, "modernbert: hip: hidden %% 64 and intermediate %% 32 required");
+  if (c.lanes != 0 && c.lanes != 4 && c.lanes != 8 && c.lanes != 16)
+    return fail(IXH_EINVAL, "modernbert: hip: lanes %d not in {0, 4, 8, 16}", c.lanes);
+  if (c.pooling != IXH_POOL_MEAN && c.pooling != IXH_POOL_CLS)
+    return fail(IXH_EINVAL, "modernbert: pooling %d not supported (mean or cls)", c.pooling);
+  return IXH_OK;
+}
+
+int weights_ready(const ixh_model *m) {
+  if (!m->weights_valid.load())
+    return fail(IXH_ESTATE, "modernbert: weights invalidated and not set again");
+  for (size_t l = 0; l < m->layers.size(); l++) {
+    const auto &L = m->layers[l];
+    if (!L.qkv.set || !L.o.set || !L.i.set || !L.omlp.set)
+      return fail(IXH_ESTATE, "modernbert: layers.%zu matrices missing", l);
+    if ((l > 0 && !L.attn_norm_set) || !L.mlp_norm_set)
+      return fail(IXH_ESTATE, "modernbert: layers.%zu norm weights missing", l);
+  }
+  if (!m->emb_norm_set || !m->final_norm_set)
+    return fail(IXH_ESTATE, "modernbert: embeddings.norm or final_norm missing");
+  if (m->emb_format < 0) return fail(IXH_ESTATE, "modernbert: embedding table missing");
+  return IXH_OK;
+}
+
+// Tables covering at least `rows` positions (size max(rows, 512) as
+// ropeFor), returned as device pointers kept alive by `hold`.
+int rope_for(ixh_model *m, int global, int rows, const float **c, const float **s,
+             std::vector<std::shared_ptr<DevBuf>> &hold) {
+  std::lock_guard<std::mutex> lk(m->rope_mu);
+  RopeTab &t = m->rope[global];
+  if (t.rows < rows || !t.cos_t) {
+    const int size = std::max(rows, 512);
+    std::vector<float> hc, hs;
+    rope_table(global ? m->cfg.global_theta : m->cfg.local_theta, m->D, size, hc, hs);
+    auto nc = std::make_shared<DevBuf>(), ns = std::make_shared<DevBuf>();
+    int rc;
+    if ((rc = nc->ensure(hc.size() * 4)) || (rc = ns->ensure(hs.size() * 4))) return rc;
+    HIPCK(hipMemcpy(nc->p, hc.data(), hc.size() * 4, hipMemcpyHostToDevice));
+    HIPCK(hipMemcpy(ns->p, hs.data(), hs.size() * 4, hipMemcpyHostToDevice));
+    t.cos_t = nc;
+    t.sin_t = ns;
+    t.rows = size;
+    t.user = false;
+  }
+  hold.push_back(t.cos_t);
+  hold.push_back(t.sin_t);
+  *c = t.cos_t->as<float>();
+  *s = t.sin_t->as<float>();
+  return IXH_OK;
+}
+
+Workspace *acquire(ixh_model *m) {
+  {
+    std::lock_guard<std::mutex> lk(m->pool_mu);
+    if (!m->pool.empty()) {
+      Workspace *w = m->pool.back();
+      m->pool.pop_back();
+      return w;
+    }
+  }
+  Workspace *w = new Workspace();
+  if (hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking) != hipSuccess) {
+    delete w;
+    return nullptr;
+  }
+  return w;
+}
+
+void release(ixh_model *m, Workspace *w) {
+  std::lock_guard<std::mutex> lk(m->pool_mu);
+  m->pool.push_back(w);
+}
+
+struct WsGuard {
+  ixh_model *m;
+  Workspace *w;
+  ~WsGuard() {
+    if (w) release(m, w);
+  }
+};
+
+__global__ void check_ids_kernel(const int32_t *ids, int N, int vocab, int *flag) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < N && (ids[t] < 0 || ids[t] >= vocab)) atomicMin(flag, t);
+}
+
+// The forward pass. ids/out are device pointers here.
+int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
+            const int32_t *offs, int B, int out_kind, float *d_out) {
+  const ixh_config &c = m->cfg;
+  const int H = c.hidden, I = c.intermediate, nh = c.heads, D = m->D;
+  const int N = offs[B];
+  const int KpH = (int)round_up(H, 64), KpI = (int)round_up(I, 64);
+  const int ldq = std::max(KpH, KpI);
+  int T = 0;
+  std::vector<int32_t> padoff(B + 1, 0);
+  std::vector<int32_t> blocks;
+  for (int b = 0; b < B; b++) {
+    const int n = offs[b + 1] - offs[b];
+    T = std::max(T, n);
+    padoff[b + 1] = padoff[b] + (int)round_up(n, kKeyPad);
+    for (int q0 = 0; q0 < n; q0 += kAttnQBlock) {
+      blocks.push_back(b);
+      blocks.push_back(q0);
+    }
+  }
+  const int Npad = padoff[B];
+  const int nblocks = (int)blocks.size() / 2;
+
+  int rc;
+  if ((rc = w->offs.ensure(4 * (B + 1))) || (rc = w->padoff.ensure(4 * (B + 1))) ||
+      (rc = w->pos.ensure(4 * (size_t)N)) || (rc = w->blocks.ensure(4 * blocks.size())) ||
+      (rc = w->x.ensure(4 * (size_t)N * H)) || (rc = w->xn.ensure(4 * (size_t)N * H)) ||
+      (rc = w->qkv.ensure(4 * (size_t)N * 3 * H)) || (rc = w->xq.ensure((size_t)N * ldq)) ||
+      (rc = w->sa.ensure(4 * (size_t)N)) || (rc = w->qq.ensure((size_t)N * H)) ||
+      (rc = w->sq.ensure(4 * (size_t)N * nh)) || (rc = w->kp.ensure((size_t)nh * Npad * D)) ||
+      (rc = w->ks.ensure(4 * (size_t)nh * Npad)) || (rc = w->vt.ensure((size_t)nh * D * Npad)) ||
+      (rc = w->vs.ensure(4 * (size_t)B * nh * D)) || (rc = w->ctx.ensure(4 * (size_t)N * H)) ||
+      (rc = w->g.ensure(4 * (size_t)N * I)))
+    return rc;
+
+  // small host-built tables through pinned memory
+  const size_t small = 4 * ((B + 1) * 2 + blocks.size());
+  if ((rc = w->host.ensure(small))) return rc;
+  int32_t *hs = (int32_t *)w->host.p;
+  memcpy(hs, offs, 4 * (B + 1));
+  memcpy(hs + B + 1, padoff.data(), 4 * (B + 1));
+  if (!blocks.empty()) memcpy(hs + 2 * (B + 1), blocks.data(), 4 * blocks.size());
+  HIPCK(hipMemcpyAsync(w->offs.p, hs, 4 * (B + 1), hipMemcpyHostToDevice, st));
+  HIPCK(hipMemcpyAsync(w->padoff.p, hs + B + 1, 4 * (B + 1), hipMemcpyHostToDevice, st));
+  if (!blocks.empty())
+    HIPCK(hipMemcpyAsync(w->blocks.p, hs + 2 * (B + 1), 4 * blocks.size(), hipMemcpyHostToDevice, st));
+
+  std::vector<std::shared_ptr<DevBuf>> hold;
+  const float *rc_g, *rs_g, *rc_l, *rs_l;
+  if ((rc = rope_for(m, 1, T, &rc_g, &rs_g, hold)) || (rc = rope_for(m, 0, T, &rc_l, &rs_l, hold)))
+    return rc;
+
+  launch_positions(w->offs.as<int32_t>(), w->padoff.as<int32_t>(), B, w->pos.as<int32_t>(), nullptr, st);
+  LAUNCHCK("positions");
+
+  // embedding gather + embeddings.norm (infer.go:361-368) -> x; layer 0's
+  // QKV reads x itself (no attn_norm, infer.go:384-389): quantise it here.
+  RowArgs ra{};
+  ra.M = N;
+  ra.H = H;
+  ra.ids = d_ids;
+  ra.emb_format = m->emb_format;
+  ra.emb_f32 = m->emb_table.as<float>();
+  ra.emb_bf16 = m->emb_table.as<uint16_t>();
+  ra.exact_slot = m->emb_exact_slot.as<int32_t>();
+  ra.exact_rows = m->emb_exact_rows.as<float>();
+  ra.emb_i8 = m->emb_table.as<int8_t>();
+  ra.emb_i8_scale = m->emb_i8_scale.as<float>();
+  ra.gamma = m->emb_norm.as<float>();
+  ra.eps = c.norm_eps;
+  ra.lanes = c.lanes;
+  ra.out = w->x.as<float>();
+  ra.q = w->xq.as<int8_t>();
+  ra.ldq = KpH;
+  ra.sa = w->sa.as<float>();
+  launch_rownorm(ra, st);
+  LAUNCHCK("embeddings");
+
+  auto gemm = [&](int epi, const Mat &M, int Kp, float *C, int ldc, int n_valid) {
+    GemmArgs g{};
+    g.A = w->xq.as<int8_t>();
+    g.lda = Kp;
+    g.B = M.q.as<int8_t>();
+    g.ldb = M.kp;
+    g.M = N;
+    g.Np = M.np;
+    g.Kp = M.kp;
+    g.sa = w->sa.as<float>();
+    g.sb = M.sb.as<float>();
+    g.zc = M.zc.as<float>();
+    g.c128 = M.c128.as<int32_t>();
+    g.C = C;
+    g.ldc = ldc;
+    g.n_valid = n_valid;
+    g.lanes = c.lanes;
+    g.n_gelu = gelu_fma_cols(I, c.lanes);
+    return g;
+  };
+
+  AttnArgs aa{};
+  aa.qkv = w->qkv.as<float>();
+  aa.H = H;
+  aa.nh = nh;
+  aa.N = N;
+  aa.offs = w->offs.as<int32_t>();
+  aa.padoff = w->padoff.as<int32_t>();
+  aa.B = B;
+  aa.scale = (float)(1.0 / std::sqrt((double)D));  // infer.go:445
+  aa.lanes = c.lanes;
+  aa.qq = w->qq.as<int8_t>();
+  aa.sq = w->sq.as<float>();
+  aa.kp = w->kp.as<int8_t>();
+  aa.ks = w->ks.as<float>();
+  aa.vt = w->vt.as<int8_t>();
+  aa.vs = w->vs.as<float>();
+  aa.Npad = Npad;
+  aa.blocks = w->blocks.as<int32_t>();
+  aa.nblocks = nblocks;
+  aa.ctx = w->ctx.as<float>();
+
+  for (int l = 0; l < c.layers; l++) {
+    const auto &L = m->layers[l];
+    const bool global = l % c.global_every == 0;  // Config.IsGlobal
+    if (l > 0) {
+      RowArgs r{};
+      r.M = N;
+      r.H = H;
+      r.x = w->x.as<float>();
+      r.gamma = L.attn_norm.as<float>();
+      r.eps = c.norm_eps;
+      r.lanes = c.lanes;
+      r.q = w->xq.as<int8_t>();
+      r.ldq = KpH;
+      r.sa = w->sa.as<float>();
+      launch_rownorm(r, st);
+      LAUNCHCK("attn_norm");
+    }
+    // QKV projection with RoPE on the queries and keys (infer.go:390-399)
+    GemmArgs g = gemm(EPI_ROPE, L.qkv, KpH, w->qkv.as<float>(), 3 * H, 3 * H);
+    g.rope_cos = global ? rc_g : rc_l;
+    g.rope_sin = global ? rs_g : rs_l;
+    g.pos = w->pos.as<int32_t>();
+    g.rope_cols = 2 * H;
+    launch_gemm(EPI_ROPE, g, st);
+    LAUNCHCK("qkv");
+    // attention (infer.go:437-518)
+    aa.window = global ? -1 : c.local_attention / 2;
+    launch_attn_prologue(aa, st);
+    LAUNCHCK("attn_prologue");
+    launch_attn_main(aa, st);
+    LAUNCHCK("attn_main");
+    // x += ctx . Wo^T (infer.go:403)
+    launch_quant_rows(w->ctx.as<float>(), H, N, H, w->xq.as<int8_t>(), KpH, w->sa.as<float>(), st);
+    LAUNCHCK("quant_ctx");
+    g = gemm(EPI_ACCUM, L.o, KpH, w->x.as<float>(), H, H);
+    launch_gemm(EPI_ACCUM, g, st);
+    LAUNCHCK("wo");
+    // mlp_norm, Wi + GeGLU, x += g . WoMLP^T (infer.go:404-424)
+    {
+      RowArgs r{};
+      r.M = N;
+      r.H = H;
+      r.x = w->x.as<float>();
+      r.gamma = L.mlp_norm.as<float>();
+      r.eps = c.norm_eps;
+      r.lanes = c.lanes;
+      r.q = w->xq.as<int8_t>();
+      r.ldq = KpH;
+      r.sa = w->sa.as<float>();
+      launch_rownorm(r, st);
+      LAUNCHCK("mlp_norm");
+    }
+    g = gemm(EPI_GEGLU, L.i, KpH, w->g.as<float>(), I, I);
+    launch_gemm(EPI_GEGLU, g, st);
+    LAUNCHCK("wi");
+    launch_quant_rows(w->g.as<float>(), I, N, I, w->xq.as<int8_t>(), KpI, w->sa.as<float>(), st);
+    LAUNCHCK("quant_g");
+    g = gemm(EPI_ACCUM, L.omlp, KpI, w->x.as<float>(), H, H);
+    launch_gemm(EPI_ACCUM, g, st);
+    LAUNCHCK("womlp");
+  }
+  // final_norm (infer.go:427), then pooling or the token states
+  {
+    RowArgs r{};
+    r.M = N;
+    r.H = H;
+    r.x = w->x.as<float>();
+    r.gamma = m->final_norm.as<float>();
+    r.eps = c.norm_eps;
+    r.lanes = c.lanes;
+    r.out = out_kind == IXH_OUT_TOKENS ? d_out : w->xn.as<float>();
+    launch_rownorm(r, st);
+    LAUNCHCK("final_norm");
+  }
+  if (out_kind == IXH_OUT_POOLED) {
+    launch_pool(w->xn.as<float>(), w->offs.as<int32_t>(), B, H, c.pooling == IXH_POOL_CLS, d_out, st);
+    LAUNCHCK("pool");
+  }
+  // tables used by queued work stay alive until the stream has run them
+  HIPCK(hipStreamSynchronize(st));
+  return IXH_OK;
+}
+
+int check_offs(const int32_t *offs, int B) {
+  if (B < 0 || (B > 0 && !offs)) return fail(IXH_EINVAL, "modernbert: inconsistent batch");
+  if (B == 0) return IXH_OK;
+  if (offs[0] != 0) return fail(IXH_EINVAL, "modernbert: inconsistent batch");
+  for (int b = 0; b < B; b++)
+    if (offs[b + 1] < offs[b]) return fail(IXH_EINVAL, "modernbert: inconsistent batch");
+  return IXH_OK;
+}
+
+int encode_host(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, int kind,
+                float *out) {
+  if (!m) return fail(IXH_EINVAL, "modernbert: nil model");
+  int rc;
+  if ((rc = check_offs(offs, B))) return rc;
+  const int N = B ? offs[B] : 0;
+  for (int t = 0; t < N; t++)
+    if (ids[t] < 0 || ids[t] >= m->cfg.vocab)
+      return fail(IXH_ERANGE, "modernbert: id %d out of vocabulary", ids[t]);
+  const int H = m->cfg.hidden;
+  if (kind == IXH_OUT_POOLED && B > 0) memset(out, 0, sizeof(float) * (size_t)B * H);
+  if (N == 0) return IXH_OK;
+  if ((rc = weights_ready(m))) return rc;
+  DEVGUARD(m->device);
+  WsGuard wg{m, acquire(m)};
+  Workspace *w = wg.w;
+  if (!w) return fail(IXH_EHIP, "modernbert: hip: stream creation failed");
+  hipStream_t st = w->stream;
+  const size_t out_elems = kind == IXH_OUT_TOKENS ? (size_t)N * H : (size_t)B * H;
+  if ((rc = w->ids.ensure(4 * (size_t)N)) || (rc = w->pooled.ensure(4 * out_elems))) return rc;
+  HIPCK(hipMemcpyAsync(w->ids.p, ids, 4 * (size_t)N, hipMemcpyHostToDevice, st));
+  if ((rc = forward(m, w, st, w->ids.as<int32_t>(), offs, B, kind, w->pooled.as<float>()))) return rc;
+  HIPCK(hipMemcpyAsync(out, w->pooled.p, 4 * out_elems, hipMemcpyDeviceToHost, st));
+  HIPCK(hipStreamSynchronize(st));
+  return IXH_OK;
+}
+
+}  // namespace
+
+// ==== C ABI =================================================================
+extern "C" {
+
+const char *ixh_last_error(void) { return g_err.c_str(); }
+
+int ixh_device_count(int *count) {
+  if (!count) return fail(IXH_EINVAL, "ixh_device_count: nil");
+  int n = 0;
+  HIPCK(hipGetDeviceCount(&n));
+  *count = n;
+  return IXH_OK;
+}
+
+int ixh_model_create(const ixh_config *cfg, int device, ixh_model **out) {
+  if (!cfg || !out) return fail(IXH_EINVAL, "modernbert: nil config");
+  int rc;
+  if ((rc = validate_config(*cfg))) return rc;
+  int n = 0;
+  HIPCK(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(IXH_EINVAL, "modernbert: hip: no device %d", device);
+  auto *m = new ixh_model();
+  m->cfg = *cfg;
+  m->device = device;
+  m->D = cfg->hidden / cfg->heads;
+  m->layers.resize(cfg->layers);
+  *out = m;
+  return IXH_OK;
+}
+
+void ixh_model_destroy(ixh_model *m) {
+  if (!m) return;
+  DeviceGuard dg(m->device);
+  delete m;
+}
+
+int ixh_model_set_matrix(ixh_model *m, int layer, int which, const int8_t *q, const float *scale,
+                         int layout) {
+  if (!m || !q || !scale) return fail(IXH_EINVAL, "modernbert: nil matrix");
+  if (layer < 0 || layer >= m->cfg.layers)
+    return fail(IXH_EINVAL, "modernbert: layer %d out of range", layer);
+  if (layout != IXH_LAYOUT_ROWS && layout != IXH_LAYOUT_PANELS)
+    return fail(IXH_EINVAL, "modernbert: layout %d", layout);
+  const int H = m->cfg.hidden, I = m->cfg.intermediate;
+  int k, n;
+  Mat *M;
+  auto &L = m->layers[layer];
+  switch (which) {
+  case IXH_MAT_QKV: k = H; n = 3 * H; M = &L.qkv; break;
+  case IXH_MAT_O: k = H; n = H; M = &L.o; break;
+  case IXH_MAT_I: k = H; n = 2 * I; M = &L.i; break;
+  case IXH_MAT_OMLP: k = I; n = H; M = &L.omlp; break;
+  default: return fail(IXH_EINVAL, "modernbert: matrix %d", which);
+  }
+  DEVGUARD(m->device);
+  std::vector<int8_t> rows = to_rows(q, k, n, layout);
+  std::vector<int> perm;
+  if (which == IXH_MAT_I) perm = geglu_perm(I);
+  return upload_mat(*M, rows, scale, k, n, which == IXH_MAT_I ? &perm : nullptr);
+}
+
+int ixh_model_set_norm(ixh_model *m, int which, int layer, const float *gamma) {
+  if (!m || !gamma) return fail(IXH_EINVAL, "modernbert: nil norm");
+  const int H = m->cfg.hidden;
+  DevBuf *dst;
+  bool *flag;
+  switch (which) {
+  case IXH_NORM_EMB: dst = &m->emb_norm; flag = &m->emb_norm_set; break;
+  case IXH_NORM_FINAL: dst = &m->final_norm; flag = &m->final_norm_set; break;
+  case IXH_NORM_ATTN:
+  case IXH_NORM_MLP:
+    if (layer < 0 || layer >= m->cfg.layers)
+      return fail(IXH_EINVAL, "modernbert: layer %d out of range", layer);
+    if (which == IXH_NORM_ATTN && layer == 0)
+      return fail(IXH_EINVAL, "modernbert: layers.0 has no attn_norm");
+    dst = which == IXH_NORM_ATTN ? &m->layers[layer].attn_norm : &m->layers[layer].mlp_norm;
+    flag = which == IXH_NORM_ATTN ? &m->layers[layer].attn_norm_set : &m->layers[layer].mlp_norm_set;
+    break;
+  default: return fail(IXH_EINVAL, "modernbert: norm %d", which);
+  }
+  DEVGUARD(m->device);
+  int rc;
+  if ((rc = dst->ensure(4 * (size_t)H))) return rc;
+  HIPCK(hipMemcpy(dst->p, gamma, 4 * (size_t)H, hipMemcpyHostToDevice));
+  *flag = true;
+  return IXH_OK;
+}
+
+int ixh_model_set_embeddings_f32(ixh_model *m, const float *table) {
+  if (!m || !table) return fail(IXH_EINVAL, "modernbert: nil table");
+  DEVGUARD(m->device);
+  const size_t bytes = 4 * (size_t)m->cfg.vocab * m->cfg.hidden;
+  int rc;
+  if ((rc = m->emb_table.ensure(bytes))) return rc;
+  HIPCK(hipMemcpy(m->emb_table.p, table, bytes, hipMemcpyHostToDevice));
+  m->emb_format = 0;
+  return IXH_OK;
+}
+
+int ixh_model_set_embeddings_bf16(ixh_model *m, const uint16_t *table, const int32_t *exact_ids,
+                                  const float *exact_rows, int n_exact) {
+  if (!m || !table || n_exact < 0 || (n_exact > 0 && (!exact_ids || !exact_rows)))
+    return fail(IXH_EINVAL, "modernbert: nil table");
+  const int V = m->cfg.vocab, H = m->cfg.hidden;
+  std::vector<int32_t> slot(V, -1);
+  for (int e = 0; e < n_exact; e++) {
+    if (exact_ids[e] < 0 || exact_ids[e] >= V)
+      return fail(IXH_EINVAL, "indecis: exact row %d out of vocabulary", exact_ids[e]);
+    slot[exact_ids[e]] = e;  // embeddings.go:38-44: a later row wins
+  }
+  DEVGUARD(m->device);
+  int rc;
+  if ((rc = m->emb_table.ensure(2 * (size_t)V * H)) || (rc = m->emb_exact_slot.ensure(4 * (size_t)V)) ||
+      (rc = m->emb_exact_rows.ensure(4 * (size_t)std::max(n_exact, 1) * H)))
+    return rc;
+  HIPCK(hipMemcpy(m->emb_table.p, table, 2 * (size_t)V * H, hipMemcpyHostToDevice));
+  HIPCK(hipMemcpy(m->emb_exact_slot.p, slot.data(), 4 * (size_t)V, hipMemcpyHostToDevice));
+  if (n_exact > 0)
+    HIPCK(hipMemcpy(m->emb_exact_rows.p, exact_rows, 4 * (size_t)n_exact * H, hipMemcpyHostToDevice));
+  m->emb_format = 1;
+  return IXH_OK;
+}
+
+int ixh_model_set_embeddings_i8(ixh_model *m, const int8_t *table, const float *row_scale) {
+  if (!m || !table || !row_scale) return fail(IXH_EINVAL, "modernbert: nil table");
+  const int V = m->cfg.vocab, H = m->cfg.hidden;
+  DEVGUARD(m->device);
+  int rc;
+  if ((rc = m->emb_table.ensure((size_t)V * H)) || (rc = m->emb_i8_scale.ensure(4 * (size_t)V)))
+    return rc;
+  HIPCK(hipMemcpy(m->emb_table.p, table, (size_t)V * H, hipMemcpyHostToDevice));
+  HIPCK(hipMemcpy(m->emb_i8_scale.p, row_scale, 4 * (size_t)V, hipMemcpyHostToDevice));
+  m->emb_format = 2;
+  return IXH_OK;
+}
+
+int ixh_model_set_rope(ixh_model *m, int is_global, const float *cos_t, const float *sin_t,
+                       int rows) {
+  if (!m || !cos_t || !sin_t || rows <= 0) return fail(IXH_EINVAL, "modernbert: nil rope table");
+  DEVGUARD(m->device);
+  const size_t bytes = 4 * (size_t)rows * (m->D / 2);
+  auto nc = std::make_shared<DevBuf>(), ns = std::make_shared<DevBuf>();
+  int rc;
+  if ((rc = nc->ensure(bytes)) || (rc = ns->ensure(bytes))) return rc;
+  HIPCK(hipMemcpy(nc->p, cos_t, bytes, hipMemcpyHostToDevice));
+  HIPCK(hipMemcpy(ns->p, sin_t, bytes, hipMemcpyHostToDevice));
+  std::lock_guard<std::mutex> lk(m->rope_mu);
+  RopeTab &t = m->rope[is_global ? 1 : 0];
+  t.cos_t = nc;
+  t.sin_t = ns;
+  t.rows = rows;
+  t.user = true;
+  return IXH_OK;
+}
+
+int ixh_model_invalidate(ixh_model *m) {
+  if (!m) return fail(IXH_EINVAL, "modernbert: nil model");
+  DEVGUARD(m->device);
+  for (auto &L : m->layers) {
+    L.qkv.set = L.o.set = L.i.set = L.omlp.set = false;
+  }
+  return IXH_OK;
+}
+
+int ixh_encode_seqs(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, float *out) {
+  return encode_host(m, ids, offs, B, IXH_OUT_POOLED, out);
+}
+
+int ixh_encode_tokens(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, float *out) {
+  return encode_host(m, ids, offs, B, IXH_OUT_TOKENS, out);
+}
+
+int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs, int B,
+                      int out_kind, float *d_out, void *stream) {
+  if (!m) return fail(IXH_EINVAL, "modernbert: nil model");
+  if (out_kind != IXH_OUT_POOLED && out_kind != IXH_OUT_TOKENS)
+    return fail(IXH_EINVAL, "modernbert: output kind %d", out_kind);
+  int rc;
+  if ((rc = check_offs(offs, B))) return rc;
+  const int N = B ? offs[B] : 0;
+  const int H = m->cfg.hidden;
+  DEVGUARD(m->device);
+  WsGuard wg{m, acquire(m)};
+  Workspace *w = wg.w;
+  if (!w) return fail(IXH_EHIP, "modernbert: hip: stream creation failed");
+  hipStream_t st = stream ? (hipStream_t)stream : w->stream;
+  if (out_kind == IXH_OUT_POOLED && B > 0)
+    HIPCK(hipMemsetAsync(d_out, 0, 4 * (size_t)B * H, st));
+  if (N == 0) return IXH_OK;
+  if ((rc = weights_ready(m))) return rc;
+  // ids on the device: checked by a kernel (infer.go:308-312)
+  if ((rc = w->flag.ensure(4)) || (rc = w->host.ensure(4))) return rc;
+  const int big = 0x7f7f7f7f;  // the byte fill below: larger than any index
+  HIPCK(hipMemsetAsync(w->flag.p, 0x7f, 4, st));
+  check_ids_kernel<<<(N + 255) / 256, 256, 0, st>>>(d_ids, N, m->cfg.vocab, w->flag.as<int>());
+  LAUNCHCK("check_ids");
+  HIPCK(hipMemcpyAsync(w->host.p, w->flag.p, 4, hipMemcpyDeviceToHost, st));
+  HIPCK(hipStreamSynchronize(st));
+  const int bad = *(const int *)w->host.p;
+  if (bad != big) {
+    int32_t id = 0;
+    HIPCK(hipMemcpy(&id, d_ids + bad, 4, hipMemcpyDeviceToHost));
+    return fail(IXH_ERANGE, "modernbert: id %d out of vocabulary", id);
+  }
+  return forward(m, w, st, d_ids, offs, B, out_kind, d_out);
+}
+
+int ixh_head_logits(ixh_model *m, const float *x, int T, const float *w, const float *b,
+                    int rows, double *z) {
+  if (!m || T < 0 || rows <= 0 || (T > 0 && (!x || !z)) || !w || !b)
+    return fail(IXH_EINVAL, "indecis: head: bad arguments");
+  if (T == 0) return IXH_OK;
+  const int H = m->cfg.hidden;
+  DEVGUARD(m->device);
+  DevBuf dx, dw, db, dz;
+  int rc;
+  if ((rc = dx.ensure(4 * (size_t)T * H)) || (rc = dw.ensure(4 * (size_t)rows * H)) ||
+      (rc = db.ensure(4 * (size_t)rows)) || (rc = dz.ensure(8 * (size_t)T * rows)))
+    return rc;
+  HIPCK(hipMemcpy(dx.p, x, 4 * (size_t)T * H, hipMemcpyHostToDevice));
+  HIPCK(hipMemcpy(dw.p, w, 4 * (size_t)rows * H, hipMemcpyHostToDevice));
+  HIPCK(hipMemcpy(db.p, b, 4 * (size_t)rows, hipMemcpyHostToDevice));
+  launch_head_logits(dx.as<float>(), T, H, dw.as<float>(), db.as<float>(), rows, dz.as<double>(), 0);
+  LAUNCHCK("head_logits");
+  HIPCK(hipDeviceSynchronize());
+  HIPCK(hipMemcpy(z, dz.p, 8 * (size_t)T * rows, hipMemcpyDeviceToHost));
+  return IXH_OK;
+}
+
+// ---- linalg -----------------------------------------------------------------
+
+int ixh_packb8_create(int device, const int8_t *q, const float *scale, int k, int n, int layout,
+                      ixh_packed_b8 **out) {
+  if (!q || !scale || !out || k <= 0 || n <= 0) return fail(IXH_EINVAL, "linalg: PackB8: bad arguments");
+  if (layout != IXH_LAYOUT_ROWS && layout != IXH_LAYOUT_PANELS)
+    return fail(IXH_EINVAL, "linalg: PackB8: layout %d", layout);
+  DEVGUARD(device);
+  auto *b = new ixh_packed_b8();
+  b->device = device;
+  b->rows = to_rows(q, k, n, layout);
+  b->scale.assign(scale, scale + n);
+  int rc = upload_mat(b->mat, b->rows, scale, k, n, nullptr);
+  if (rc) {
+    delete b;
+    return rc;
+  }
+  *out = b;
+  return IXH_OK;
+}
+
+void ixh_packb8_destroy(ixh_packed_b8 *b) {
+  if (!b) return;
+  DeviceGuard dg(b->device);
+  delete b;
+}
+
+namespace {
+// Uploads a [m][k] f32 with rows padded to ld = roundup(k, 4), quantises
+// it into q [m][Kp] (zero padding) and sa [m] on stream st.
+int quantize_upload(const float *a, int m, int k, int Kp, DevBuf &da, DevBuf &dq, DevBuf &dsa,
+                    hipStream_t st) {
+  const int ld = (int)round_up(k, 4);
+  int rc;
+  if ((rc = da.ensure(4 * (size_t)m * ld)) || (rc = dq.ensure((size_t)m * Kp)) ||
+      (rc = dsa.ensure(4 * (size_t)m)))
+    return rc;
+  if (ld == k) {
+    HIPCK(hipMemcpyAsync(da.p, a, 4 * (size_t)m * k, hipMemcpyHostToDevice, st));
+  } else {
+    HIPCK(hipMemsetAsync(da.p, 0, 4 * (size_t)m * ld, st));
+    HIPCK(hipMemcpy2DAsync(da.p, 4 * (size_t)ld, a, 4 * (size_t)k, 4 * (size_t)k, m,
+                           hipMemcpyHostToDevice, st));
+  }
+  launch_quant_rows(da.as<float>(), ld, m, ld, dq.as<int8_t>(), Kp, dsa.as<float>(), st);
+  LAUNCHCK("quant_rows");
+  return IXH_OK;
+}
+
+struct TmpStream {
+  hipStream_t s = nullptr;
+  ~TmpStream() {
+    if (s) (void)hipStreamDestroy(s);
+  }
+};
+}  // namespace
+
+int ixh_matmul8(ixh_packed_b8 *b, float *c, const float *a, int m, int accumulate) {
+  if (!b || m < 0 || (m > 0 && (!c || !a))) return fail(IXH_EINVAL, "linalg: MatMul8: slice too short");
+  if (m == 0) return IXH_OK;
+  DEVGUARD(b->device);
+  TmpStream ts;
+  HIPCK(hipStreamCreateWithFlags(&ts.s, hipStreamNonBlocking));
+  const Mat &M = b->mat;
+  DevBuf da, dq, dsa, dc;
+  int rc;
+  if ((rc = quantize_upload(a, m, M.k, M.kp, da, dq, dsa, ts.s))) return rc;
+  if ((rc = dc.ensure(4 * (size_t)m * M.n))) return rc;
+  if (accumulate) HIPCK(hipMemcpyAsync(dc.p, c, 4 * (size_t)m * M.n, hipMemcpyHostToDevice, ts.s));
+  GemmArgs g{};
+  g.A = dq.as<int8_t>();
+  g.lda = M.kp;
+  g.B = M.q.as<int8_t>();
+  g.ldb = M.kp;
+  g.M = m;
+  g.Np = M.np;
+  g.Kp = M.kp;
+  g.sa = dsa.as<float>();
+  g.sb = M.sb.as<float>();
+  g.zc = M.zc.as<float>();
+  g.c128 = M.c128.as<int32_t>();
+  g.C = dc.as<float>();
+  g.ldc = M.n;
+  g.n_valid = M.n;
+  launch_gemm(accumulate ? EPI_ACCUM : EPI_STORE, g, ts.s);
+  LAUNCHCK("matmul8");
+  HIPCK(hipMemcpyAsync(c, dc.p, 4 * (size_t)m * M.n, hipMemcpyDeviceToHost, ts.s));
+  HIPCK(hipStreamSynchronize(ts.s));
+  return IXH_OK;
+}
+
+int ixh_matmul8_tile(ixh_packed_b8 *b, const float *a, int m, int8_t *aq, float *sa,
+                     int32_t *tile) {
+  if (!b || m < 0 || (m > 0 && !a)) return fail(IXH_EINVAL, "linalg: MatMul8: slice too short");
+  if (m == 0) return IXH_OK;
+  DEVGUARD(b->device);
+  TmpStream ts;
+  HIPCK(hipStreamCreateWithFlags(&ts.s, hipStreamNonBlocking));
+  const Mat &M = b->mat;
+  DevBuf da, dq, dsa, dt;
+  int rc;
+  if ((rc = quantize_upload(a, m, M.k, M.kp, da, dq, dsa, ts.s))) return rc;
+  if (tile) {
+    if ((rc = dt.ensure(4 * (size_t)m * M.n))) return rc;
+    GemmArgs g{};
+    g.A = dq.as<int8_t>();
+    g.lda = M.kp;
+    g.B = M.q.as<int8_t>();
+    g.ldb = M.kp;
+    g.M = m;
+    g.Np = M.np;
+    g.Kp = M.kp;
+    g.sa = dsa.as<float>();
+    g.sb = M.sb.as<float>();
+    g.zc = M.zc.as<float>();
+    g.c128 = M.c128.as<int32_t>();
+    g.Ci = dt.as<int32_t>();
+    g.ldc = M.n;
+    g.n_valid = M.n;
+    launch_gemm(EPI_TILE, g, ts.s);
+    LAUNCHCK("matmul8_tile");
+    HIPCK(hipMemcpyAsync(tile, dt.p, 4 * (size_t)m * M.n, hipMemcpyDeviceToHost, ts.s));
+  }
+  if (aq)
+    HIPCK(hipMemcpy2DAsync(aq, (size_t)M.k, dq.p, (size_t)M.kp, (size_t)M.k, m, hipMemcpyDeviceToHost, ts.s));
+  if (sa) HIPCK(hipMemcpyAsync(sa, dsa.p, 4 * (size_t)m, hipMemcpyDeviceToHost, ts.s));
+  HIPCK(hipStreamSynchronize(ts.s));
+  return IXH_OK;
+}
+
+int ixh_layernorm_quant(int device, const float *x, int m, int h, const float *gamma, double eps,
+                        int lanes, float *out, int8_t *q, float *sa) {
+  if (m < 0 || h <= 0 || (m > 0 && (!x || !gamma)) || (q && !sa))
+    return fail(IXH_EINVAL, "linalg: LayerNormRow: bad arguments");
+  if (h % 4 != 0) return fail(IXH_EINVAL, "linalg: hip: LayerNormRow needs rows of a multiple of 4 values");
+  if (lanes != 0 && lanes != 4 && lanes != 8 && lanes != 16)
+    return fail(IXH_EINVAL, "linalg: hip: lanes %d not in {0, 4, 8, 16}", lanes);
+  if (m == 0) return IXH_OK;
+  DEVGUARD(device);
+  TmpStream ts;
+  HIPCK(hipStreamCreateWithFlags(&ts.s, hipStreamNonBlocking));
+  DevBuf dx, dg, dout, dq, dsa;
+  int rc;
+  if ((rc = dx.ensure(4 * (size_t)m * h)) || (rc = dg.ensure(4 * (size_t)h)) ||
+      (rc = dout.ensure(4 * (size_t)m * h)) || (rc = dq.ensure((size_t)m * h)) ||
+      (rc = dsa.ensure(4 * (size_t)m)))
+    return rc;
+  HIPCK(hipMemcpyAsync(dx.p, x, 4 * (size_t)m * h, hipMemcpyHostToDevice, ts.s));
+  HIPCK(hipMemcpyAsync(dg.p, gamma, 4 * (size_t)h, hipMemcpyHostToDevice, ts.s));
+  RowArgs r{};
+  r.M = m;
+  r.H = h;
+  r.x = dx.as<float>();
+  r.gamma = dg.as<float>();
+  r.eps = eps;
+  r.lanes = lanes;
+  r.out = out ? dout.as<float>() : nullptr;
+  r.q = q ? dq.as<int8_t>() : nullptr;
+  r.ldq = h;
+  r.sa = dsa.as<float>();
+  launch_rownorm(r, ts.s);
+  LAUNCHCK("layernorm_quant");
+  if (out) HIPCK(hipMemcpyAsync(out, dout.p, 4 * (size_t)m * h, hipMemcpyDeviceToHost, ts.s));
+  if (q) {
+    HIPCK(hipMemcpyAsync(q, dq.p, (size_t)m * h, hipMemcpyDeviceToHost, ts.s));
+    HIPCK(hipMemcpyAsync(sa, dsa.p, 4 * (size_t)m, hipMemcpyDeviceToHost, ts.s));
+  }
+  HIPCK(hipStreamSynchronize(ts.s));
+  return IXH_OK;
+}
+
+int ixh_ln_matmul8_geglu(ixh_packed_b8 *b, const float *x, int m, const float *gamma, double eps,
+                         int lanes, float *g, int32_t *tile) {
+  if (!b || m < 0 || (m > 0 && (!x || !gamma || !g)))
+    return fail(IXH_EINVAL, "linalg: GeluMul: bad arguments");
+  const int k = b->mat.k, n = b->mat.n;
+  if (n % 64 != 0) return fail(IXH_EINVAL, "linalg: hip: GeGLU needs n/2 a multiple of 32");
+  if (k % 4 != 0) return fail(IXH_EINVAL, "linalg: hip: LayerNormRow needs rows of a multiple of 4 values");
+  if (lanes != 0 && lanes != 4 && lanes != 8 && lanes != 16)
+    return fail(IXH_EINVAL, "linalg: hip: lanes %d not in {0, 4, 8, 16}", lanes);
+  if (m == 0) return IXH_OK;
+  DEVGUARD(b->device);
+  {
+    std::lock_guard<std::mutex> lk(b->mu);
+    if (!b->geglu_set) {
+      std::vector<int> perm = geglu_perm(n / 2);
+      int rc = upload_mat(b->geglu, b->rows, b->scale.data(), k, n, &perm);
+      if (rc) return rc;
+      b->geglu_set = true;
+    }
+  }
+  TmpStream ts;
+  HIPCK(hipStreamCreateWithFlags(&ts.s, hipStreamNonBlocking));
+  const Mat &M = b->geglu;
+  DevBuf dx, dgam, dq, dsa, dg, dt;
+  int rc;
+  if ((rc = dx.ensure(4 * (size_t)m * k)) || (rc = dgam.ensure(4 * (size_t)k)) ||
+      (rc = dq.ensure((size_t)m * M.kp)) || (rc = dsa.ensure(4 * (size_t)m)) ||
+      (rc = dg.ensure(4 * (size_t)m * (n / 2))))
+    return rc;
+  HIPCK(hipMemcpyAsync(dx.p, x, 4 * (size_t)m * k, hipMemcpyHostToDevice, ts.s));
+  HIPCK(hipMemcpyAsync(dgam.p, gamma, 4 * (size_t)k, hipMemcpyHostToDevice, ts.s));
+  RowArgs r{};
+  r.M = m;
+  r.H = k;
+  r.x = dx.as<float>();
+  r.gamma = dgam.as<float>();
+  r.eps = eps;
+  r.lanes = lanes;
+  r.q = dq.as<int8_t>();
+  r.ldq = M.kp;
+  r.sa = dsa.as<float>();
+  launch_rownorm(r, ts.s);
+  LAUNCHCK("layernorm_quant");
+  GemmArgs ga{};
+  ga.A = dq.as<int8_t>();
+  ga.lda = M.kp;
+  ga.B = M.q.as<int8_t>();
+  ga.ldb = M.kp;
+  ga.M = m;
+  ga.Np = M.np;
+  ga.Kp = M.kp;
+  ga.sa = dsa.as<float>();
+  ga.sb = M.sb.as<float>();
+  ga.zc = M.zc.as<float>();
+  ga.c128 = M.c128.as<int32_t>();
+  ga.C = dg.as<float>();
+  ga.ldc = n / 2;
+  ga.n_valid = n / 2;
+  ga.lanes = lanes;
+  ga.n_gelu = gelu_fma_cols(n / 2, lanes);
+  launch_gemm(EPI_GEGLU, ga, ts.s);
+  LAUNCHCK("geglu");
+  HIPCK(hipMemcpyAsync(g, dg.p, 4 * (size_t)m * (n / 2), hipMemcpyDeviceToHost, ts.s));
+  if (tile) {
+    // the reference tile of the natural (un-interleaved) matrix
+    const Mat &N0 = b->mat;
+    if ((rc = dt.ensure(4 * (size_t)m * n))) return rc;
+    GemmArgs gt = ga;
+    gt.B = N0.q.as<int8_t>();
+    gt.Np = N0.np;
+    gt.sb = N0.sb.as<float>();
+    gt.zc = N0.zc.as<float>();
+    gt.c128 = N0.c128.as<int32_t>();
+    gt.Ci = dt.as<int32_t>();
+    gt.C = nullptr;
+    gt.ldc = n;
+    gt.n_valid = n;
+    launch_gemm(EPI_TILE, gt, ts.s);
+    LAUNCHCK("geglu_tile");
+    HIPCK(hipMemcpyAsync(tile, dt.p, 4 * (size_t)m * n, hipMemcpyDeviceToHost, ts.s));
+  }
+  HIPCK(hipStreamSynchronize(ts.s));
+  return IXH_OK;
+}
+
+int ixh_attend8(int device, float *o, const float *q, const float *k, const float *v, int n, int d,
+                int window, float scale, int lanes) {
+  if (n < 0 || (n > 0 && (!o || !q || !k || !v))) return fail(IXH_EINVAL, "linalg: Attend8: bad arguments");
+  if (d != 64) return fail(IXH_EINVAL, "linalg: hip: Attend8 head dimension %d not supported (64)", d);
+  if (lanes != 0 && lanes != 4 && lanes != 8 && lanes != 16)
+    return fail(IXH_EINVAL, "linalg: hip: lanes %d not in {0, 4, 8, 16}", lanes);
+  if (n == 0) return IXH_OK;
+  DEVGUARD(device);
+  TmpStream ts;
+  HIPCK(hipStreamCreateWithFlags(&ts.s, hipStreamNonBlocking));
+  const int H = 64, Npad = (int)round_up(n, kKeyPad);
+  std::vector<float> qkv((size_t)n * 3 * H);
+  for (int j = 0; j < n; j++) {
+    memcpy(&qkv[(size_t)j * 3 * H], q + (size_t)j * d, 4 * d);
+    memcpy(&qkv[(size_t)j * 3 * H + H], k + (size_t)j * d, 4 * d);
+    memcpy(&qkv[(size_t)j * 3 * H + 2 * H], v + (size_t)j * d, 4 * d);
+  }
+  std::vector<int32_t> tabs = {0, n, 0, Npad};
+  std::vector<int32_t> blocks;
+  for (int q0 = 0; q0 < n; q0 += kAttnQBlock) {
+    blocks.push_back(0);
+    blocks.push_back(q0);
+  }
+  DevBuf dqkv, dtabs, dblocks, dqq, dsq, dkp, dks, dvt, dvs, dctx;
+  int rc;
+  if ((rc = dqkv.ensure(4 * qkv.size())) || (rc = dtabs.ensure(16)) ||
+      (rc = dblocks.ensure(4 * blocks.size())) || (rc = dqq.ensure((size_t)n * H)) ||
+      (rc = dsq.ensure(4 * (size_t)n)) || (rc = dkp.ensure((size_t)Npad * H)) ||
+      (rc = dks.ensure(4 * (size_t)Npad)) || (rc = dvt.ensure((size_t)H * Npad)) ||
+      (rc = dvs.ensure(4 * H)) || (rc = dctx.ensure(4 * (size_t)n * H)))
+    return rc;
+  HIPCK(hipMemcpyAsync(dqkv.p, qkv.data(), 4 * qkv.size(), hipMemcpyHostToDevice, ts.s));
+  HIPCK(hipMemcpyAsync(dtabs.p, tabs.data(), 16, hipMemcpyHostToDevice, ts.s));
+  HIPCK(hipMemcpyAsync(dblocks.p, blocks.data(), 4 * blocks.size(), hipMemcpyHostToDevice, ts.s));
+  AttnArgs aa{};
+  aa.qkv = dqkv.as<float>();
+  aa.H = H;
+  aa.nh = 1;
+  aa.N = n;
+  aa.offs = dtabs.as<int32_t>();
+  aa.padoff = dtabs.as<int32_t>() + 2;
+  aa.B = 1;
+  aa.scale = scale;
+  aa.window = window;
+  aa.lanes = lanes;
+  aa.qq = dqq.as<int8_t>();
+  aa.sq = dsq.as<float>();
+  aa.kp = dkp.as<int8_t>();
+  aa.ks = dks.as<float>();
+  aa.vt = dvt.as<int8_t>();
+  aa.vs = dvs.as<float>();
+  aa.Npad = Npad;
+  aa.blocks = dblocks.as<int32_t>();
+  aa.nblocks = (int)blocks.size() / 2;
+  aa.ctx = dctx.as<float>();
+  launch_attn_prologue(aa, ts.s);
+  LAUNCHCK("attn_prologue");
+  launch_attn_main(aa, ts.s);
+  LAUNCHCK("attn_main");
+  HIPCK(hipMemcpyAsync(o, dctx.p, 4 * (size_t)n * H, hipMemcpyDeviceToHost, ts.s));
+  HIPCK(hipStreamSynchronize(ts.s));
+  return IXH_OK;
+}
+
+}  // extern "C"

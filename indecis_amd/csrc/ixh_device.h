@@ -1,0 +1,117 @@
+// ixh_device.h — device-side numerics shared by the gfx950 kernels.
+//
+// Every float operation here is rounded where the reference rounds it
+// (the sources are compiled with -ffp-contract=off): __builtin_fmaf where
+// the reference fuses (Go SIMD MulAdd, VFMADD213PS), separate operations
+// where it does not. IEEE division (HIP's default correctly rounded f32
+// divide) and RNE conversions throughout.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ixh {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// 32x32x32 int8 MFMA (gfx950): D[i][j] = sum_k A[i][k] B[k][j] + C.
+// Lane l supplies row i = l%32 of A and column j = l%32 of B, 16 bytes
+// each, over the same 16 values of k (lanes 0-31 one half of k, 32-63 the
+// other). D: lane l holds column j = l%32, rows 8*(r/4) + 4*(l/32) + r%4
+// for r = 0..15.
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ int acc_row(int r, int lane) {
+  return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+}
+
+__device__ __forceinline__ float fmax32(float a, float b) { return b > a ? b : a; }
+__device__ __forceinline__ float fmin32(float a, float b) { return b < a ? b : a; }
+
+// roundHalfEven (linalg/int8.go:207-210) == VCVTPS2DQ for |v| < 2^22.
+__device__ __forceinline__ float rne(float v) { return __builtin_rintf(v); }
+
+// RNE(x * inv) as int8 (QuantizeRow / quantRowAVX2 / quantColsAVX2).
+__device__ __forceinline__ int q8(float x, float inv) { return (int)rne(x * inv); }
+
+// exp32 (linalg/fastmath.go:36-52): separate roundings.
+__device__ __forceinline__ float exp32_scalar(float x) {
+  if (x < -87.3f) return 0.0f;
+  x = fmin32(x, 88.7f);
+  float n = rne(x * 1.44269504088896341f);
+  float r = x - n * 0.693359375f - n * -2.12194440e-4f;
+  float p = 1.9875691500e-4f;
+  p = p * r + 1.3981999507e-3f;
+  p = p * r + 8.3334519073e-3f;
+  p = p * r + 4.1665795894e-2f;
+  p = p * r + 1.6666665459e-1f;
+  p = p * r + 5.0000001201e-1f;
+  float y = p * r * r + r + 1.0f;
+  return y * __int_as_float(((int)n + 127) << 23);
+}
+
+// One lane of ExpShift's vector body (linalg/vec_simd.go:235-248).
+__device__ __forceinline__ float exp32_simd(float v) {
+  bool under = v < -87.3f;
+  v = fmin32(fmax32(v, -87.3f), 88.7f);
+  const float magic = 12582912.0f;
+  float n = __builtin_fmaf(v, 1.44269504088896341f, magic) - magic;
+  float r = __builtin_fmaf(n, -0.693359375f, v);
+  r = __builtin_fmaf(n, 2.12194440e-4f, r);
+  float p = __builtin_fmaf(r, 1.9875691500e-4f, 1.3981999507e-3f);
+  p = __builtin_fmaf(r, p, 8.3334519073e-3f);
+  p = __builtin_fmaf(r, p, 4.1665795894e-2f);
+  p = __builtin_fmaf(r, p, 1.6666665459e-1f);
+  p = __builtin_fmaf(r, p, 5.0000001201e-1f);
+  float y = __builtin_fmaf(p * r, r, r) + 1.0f;
+  float pw = __int_as_float(((int)n + 127) << 23);
+  return under ? 0.0f : y * pw;
+}
+
+// GELU (erf) of geluMulAVX2 (linalg/gelu_amd64.s:173-195).
+__device__ __forceinline__ float gelu_fma(float x) {
+  float t = x * 0.7071067811865476f;
+  t = fmin32(fmax32(t, -4.0f), 4.0f);
+  float t2 = t * t;
+  float p = __builtin_fmaf(t2, -2.72614225801306e-10f, 2.77068142495902e-08f);
+  p = __builtin_fmaf(t2, p, -2.10102402082508e-06f);
+  p = __builtin_fmaf(t2, p, -5.69250639462346e-05f);
+  p = __builtin_fmaf(t2, p, -7.34990630326855e-04f);
+  p = __builtin_fmaf(t2, p, -2.95459980854025e-03f);
+  p = __builtin_fmaf(t2, p, -1.60960333262415e-02f);
+  p = p * t;
+  float q = __builtin_fmaf(t2, -1.45660718464996e-05f, -2.13374055278905e-04f);
+  q = __builtin_fmaf(t2, q, -1.68282697438203e-03f);
+  q = __builtin_fmaf(t2, q, -7.37332916720468e-03f);
+  q = __builtin_fmaf(t2, q, -1.42647390514189e-02f);
+  return (0.5f * x) * (1.0f + p / q);
+}
+
+// geluScalar (linalg/fastmath.go:9-26): separate roundings.
+__device__ __forceinline__ float gelu_scalar(float x) {
+  float e = x * 0.7071067811865476f;
+  e = fmin32(fmax32(e, -4.0f), 4.0f);
+  float x2 = e * e;
+  float p = x2 * -2.72614225801306e-10f + 2.77068142495902e-08f;
+  p = x2 * p + -2.10102402082508e-06f;
+  p = x2 * p + -5.69250639462346e-05f;
+  p = x2 * p + -7.34990630326855e-04f;
+  p = x2 * p + -2.95459980854025e-03f;
+  p = x2 * p + -1.60960333262415e-02f;
+  p = p * e;
+  float q = x2 * -1.45660718464996e-05f + -2.13374055278905e-04f;
+  q = x2 * q + -1.68282697438203e-03f;
+  q = x2 * q + -7.37332916720468e-03f;
+  q = x2 * q + -1.42647390514189e-02f;
+  return 0.5f * x * (1.0f + p / q);
+}
+
+// Dequantisation of one int8 GEMM result (kernel_vnni_amd64.s:144-200):
+// f32(tile) - zc, times sb, times sa — tile being the reference's
+// unsigned-offset integer sum.
+__device__ __forceinline__ float deq(int tile, float zc, float sb, float sa) {
+  return (((float)tile - zc) * sb) * sa;
+}
+
+}  // namespace ixh

@@ -1,0 +1,112 @@
+// ixh_internal.h — kernel launchers shared by the C-ABI (ixh_api.cpp) and
+// the kernel sources. Host-side only types; no torch, no reference code.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ixh {
+
+// ---- int8 GEMM ----------------------------------------------------------
+// C = epilogue(A . B^T): A int8 [M][lda] (signed activations, zero
+// padding to Kp), B int8 [Np][ldb] (weights, one row per output channel,
+// zero padding), Kp a multiple of 64, Np a multiple of 128.
+enum GemmEpi {
+  EPI_STORE = 0,   // C[m][n] = deq
+  EPI_ACCUM = 1,   // C[m][n] += deq            (Wo, WoMLP residual)
+  EPI_TILE = 2,    // Ci[m][n] = reference int32 tile (tests)
+  EPI_GEGLU = 3,   // G[m][j] = gelu(deq a)*deq b, B rows interleaved by 32
+  EPI_ROPE = 4,    // C[m][n] = deq, RoPE on columns < rope_cols
+};
+
+struct GemmArgs {
+  const int8_t *A;
+  int lda;
+  const int8_t *B;
+  int ldb;
+  int M, Np, Kp;
+  const float *sa;       // [M]
+  const float *sb;       // [Np]
+  const float *zc;       // [Np] 128*colsum as float
+  const int32_t *c128;   // [Np] 128*colsum
+  float *C;              // EPI_STORE/ACCUM/ROPE: [M][ldc]; EPI_GEGLU: [M][ldc] gated
+  int ldc;
+  int32_t *Ci;           // EPI_TILE
+  int n_valid;           // output columns stored (of the B rows; GEGLU: gated cols)
+  // EPI_ROPE
+  const float *rope_cos, *rope_sin;  // [rows][32]
+  const int32_t *pos;                // [M]
+  int rope_cols;                     // columns < rope_cols are rotated (2H)
+  int lanes;                         // Go simd width, for the GeGLU tail rule
+  int n_gelu;                        // GEGLU: I (gated width), for the tail rule
+};
+
+void launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
+
+// ---- row kernels ----------------------------------------------------------
+struct RowArgs {
+  int M, H;
+  const float *x;          // [M][H] input (unless gather)
+  // gather (embedding row, internal/modernbert/infer.go:52-59)
+  const int32_t *ids;
+  int emb_format;          // 0 f32, 1 bf16 (+exact rows), 2 int8 (+row scale)
+  const float *emb_f32;
+  const uint16_t *emb_bf16;
+  const int32_t *exact_slot; // [V] -1 or index into exact_rows
+  const float *exact_rows;
+  const int8_t *emb_i8;
+  const float *emb_i8_scale;
+  const float *gamma;      // LayerNorm weight, nullptr: no LayerNorm
+  double eps;
+  int lanes;
+  float *out;              // [M][H] f32 result, or nullptr
+  int8_t *q;               // [M][ldq] quantised result, or nullptr
+  int ldq;
+  float *sa;               // [M]
+};
+void launch_rownorm(const RowArgs &a, hipStream_t s);
+
+// Per-row int8 quantisation (quantizeA) of f32 rows [M][ld] into [M][ldq].
+void launch_quant_rows(const float *x, int ld, int M, int K, int8_t *q, int ldq,
+                       float *sa, hipStream_t s);
+
+// Token positions and padded key slots from cumulative offsets.
+void launch_positions(const int32_t *offs, const int32_t *padoff, int B,
+                      int32_t *pos, int32_t *slot, hipStream_t s);
+
+// Mean (float64 accumulation) or first-token pooling, [B][H].
+void launch_pool(const float *xn, const int32_t *offs, int B, int H, int cls,
+                 float *out, hipStream_t s);
+
+// head.logits (heads.go:63-74) over T rows.
+void launch_head_logits(const float *x, int T, int H, const float *w,
+                        const float *b, int rows, double *z, hipStream_t s);
+
+// ---- attention ------------------------------------------------------------
+struct AttnArgs {
+  const float *qkv;        // [N][3H], RoPE applied
+  int H, nh, N;
+  const int32_t *offs;     // [B+1]
+  const int32_t *padoff;   // [B+1] start of each sequence's key slots
+  int B;
+  float scale;             // 1/sqrt(D)
+  int window;              // <0 global
+  int lanes;
+  // prologue outputs / main inputs
+  int8_t *qq;              // [N][H]
+  float *sq;               // [N][nh]
+  int8_t *kp;              // [nh][Npad][64]
+  float *ks;               // [nh][Npad]
+  int8_t *vt;              // [nh][64][Npad]
+  float *vs;               // [B][nh][64]
+  int Npad;
+  const int32_t *blocks;   // [nblocks][2]: (sequence, first query)
+  int nblocks;
+  float *ctx;              // [N][H]
+};
+void launch_attn_prologue(const AttnArgs &a, hipStream_t s);
+void launch_attn_main(const AttnArgs &a, hipStream_t s);
+
+constexpr int kAttnQBlock = 128;  // queries per workgroup (4 waves x 32)
+constexpr int kKeyPad = 64;       // key slots of a sequence are padded to this
+
+}  // namespace ixh

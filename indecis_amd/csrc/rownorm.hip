@@ -1,0 +1,288 @@
+// rownorm.hip — bandwidth-bound row kernels: embedding gather, LayerNorm,
+// per-row int8 quantisation, pooling and decision-head logits.
+//
+// LayerNorm follows linalg.LayerNormRow (linalg/vec_simd.go:285-327): the
+// reference keeps V float32 lane partials (V = the Go simd width of its
+// host) filled sequentially, adds them in float64, and does the same for
+// the fused d*d + sq. Those chains are sequential by definition, so a row
+// is owned by V/4 threads, each carrying 4 lane partials with float4 loads
+// (lanes == 0 is the scalar float64 build, vec_scalar.go:66-81, one thread
+// per row).
+#include "ixh_device.h"
+#include "ixh_internal.h"
+
+namespace ixh {
+
+namespace {
+
+struct RowSrc {
+  const RowArgs &a;
+  const float *f32;      // row base (f32 input, f32 table or exact row)
+  const uint16_t *bf16;  // row base of a bf16 table
+  const int8_t *i8;      // row base of an int8 table
+  float i8s;
+
+  __device__ RowSrc(const RowArgs &args, int r) : a(args), f32(nullptr), bf16(nullptr), i8(nullptr), i8s(0.f) {
+    if (!a.ids) {
+      f32 = a.x + (size_t)r * a.H;
+      return;
+    }
+    const int id = a.ids[r];
+    switch (a.emb_format) {
+    case 1: {
+      const int slot = a.exact_slot[id];
+      if (slot >= 0)
+        f32 = a.exact_rows + (size_t)slot * a.H;
+      else
+        bf16 = a.emb_bf16 + (size_t)id * a.H;
+      break;
+    }
+    case 2:
+      i8 = a.emb_i8 + (size_t)id * a.H;
+      i8s = a.emb_i8_scale[id];
+      break;
+    default:
+      f32 = a.emb_f32 + (size_t)id * a.H;
+    }
+  }
+  // Four consecutive values at i (i % 4 == 0): embeddings.go:48-68.
+  __device__ float4 load4(int i) const {
+    if (f32) return *(const float4 *)(f32 + i);
+    if (bf16) {
+      const uint2 u = *(const uint2 *)(bf16 + i);
+      return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                         __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+    }
+    const int w = *(const int *)(i8 + i);
+    return make_float4((float)(int8_t)(w & 0xff) * i8s, (float)(int8_t)((w >> 8) & 0xff) * i8s,
+                       (float)(int8_t)((w >> 16) & 0xff) * i8s, (float)(int8_t)(w >> 24) * i8s);
+  }
+  __device__ float load1(int i) const {
+    if (f32) return f32[i];
+    if (bf16) return __uint_as_float((unsigned)bf16[i] << 16);
+    return (float)i8[i] * i8s;
+  }
+};
+
+// TPR threads per row (lanes/4), or 1 for the scalar (lanes == 0) build.
+template <int TPR>
+__global__ __launch_bounds__(256) void rownorm_kernel(RowArgs a) {
+  const int gt = blockIdx.x * blockDim.x + threadIdx.x;
+  const int r = gt / TPR, sub = gt % TPR;
+  if (r >= a.M) return;  // whole groups exit together (TPR divides 64)
+  const RowSrc src(a, r);
+  const int H = a.H;
+  const int V = TPR * 4;
+  const bool scalar = a.lanes <= 0;
+  const int main_end = scalar ? 0 : (H / V) * V;
+
+  float mean = 0.f, rstd = 1.f;
+  const bool ln = a.gamma != nullptr;
+  if (ln) {
+    double sum = 0.0;
+    if (scalar) {
+      for (int i = 0; i < H; i++) sum += (double)src.load1(i);
+    } else {
+      float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+      for (int i = 4 * sub; i < main_end; i += V) {
+        const float4 v = src.load4(i);
+        p0 = p0 + v.x; p1 = p1 + v.y; p2 = p2 + v.z; p3 = p3 + v.w;
+      }
+      // lanes summed in float64 in lane order (vec_simd.go:294-297)
+      for (int t = 0; t < TPR; t++) {
+        sum += (double)__shfl(p0, t, TPR);
+        sum += (double)__shfl(p1, t, TPR);
+        sum += (double)__shfl(p2, t, TPR);
+        sum += (double)__shfl(p3, t, TPR);
+      }
+      for (int i = main_end; i < H; i++) sum += (double)src.load1(i);
+    }
+    mean = (float)(sum / (double)H);
+    double var = 0.0;
+    if (scalar) {
+      for (int i = 0; i < H; i++) {
+        const double d = (double)(src.load1(i) - mean);
+        var += d * d;
+      }
+    } else {
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+      for (int i = 4 * sub; i < main_end; i += V) {
+        const float4 v = src.load4(i);
+        const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
+        s0 = __builtin_fmaf(d0, d0, s0);
+        s1 = __builtin_fmaf(d1, d1, s1);
+        s2 = __builtin_fmaf(d2, d2, s2);
+        s3 = __builtin_fmaf(d3, d3, s3);
+      }
+      for (int t = 0; t < TPR; t++) {
+        var += (double)__shfl(s0, t, TPR);
+        var += (double)__shfl(s1, t, TPR);
+        var += (double)__shfl(s2, t, TPR);
+        var += (double)__shfl(s3, t, TPR);
+      }
+      for (int i = main_end; i < H; i++) {
+        const double d = (double)(src.load1(i) - mean);
+        var += d * d;
+      }
+    }
+    rstd = (float)(1.0 / __builtin_sqrt(var / (double)H + a.eps));
+  }
+
+  // Output pass(es): o = ((x - mean) * rstd) * gamma. Each thread owns the
+  // columns 4*sub + V*k (+ the tail for sub 0; every column if scalar).
+  auto out_at = [&](int i, float x) -> float {
+    return ln ? ((x - mean) * rstd) * a.gamma[i] : x;
+  };
+  const int step = scalar ? 4 : V;
+  const int first = scalar ? 0 : 4 * sub;
+  const int vec_end = scalar ? (H & ~3) : main_end;
+  const int tail_begin = vec_end;
+  const bool do_tail = scalar || sub == 0;
+  float mx = 0.f;
+  for (int i = first; i < vec_end; i += step) {
+    const float4 v = src.load4(i);
+    const float o0 = out_at(i, v.x), o1 = out_at(i + 1, v.y), o2 = out_at(i + 2, v.z),
+                o3 = out_at(i + 3, v.w);
+    if (a.out) *(float4 *)(a.out + (size_t)r * H + i) = make_float4(o0, o1, o2, o3);
+    mx = fmax32(mx, fmax32(fmax32(fabsf(o0), fabsf(o1)), fmax32(fabsf(o2), fabsf(o3))));
+  }
+  if (do_tail)
+    for (int i = tail_begin; i < H; i++) {
+      const float o = out_at(i, src.load1(i));
+      if (a.out) a.out[(size_t)r * H + i] = o;
+      mx = fmax32(mx, fabsf(o));
+    }
+  if (!a.q) return;
+  for (int t = 1; t < TPR; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t, TPR));
+  // quantizeA (linalg/int8.go:160-191): scale = max/127, inv = 1/scale.
+  float s = 0.f, inv = 0.f;
+  if (mx != 0.f) {
+    s = mx / 127.0f;
+    inv = 1.0f / s;
+  }
+  int8_t *qrow = a.q + (size_t)r * a.ldq;
+  for (int i = first; i < vec_end; i += step) {
+    const float4 v = src.load4(i);
+    const int q0 = q8(out_at(i, v.x), inv), q1 = q8(out_at(i + 1, v.y), inv);
+    const int q2 = q8(out_at(i + 2, v.z), inv), q3 = q8(out_at(i + 3, v.w), inv);
+    *(int *)(qrow + i) = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+  }
+  if (do_tail) {
+    for (int i = tail_begin; i < H; i++) qrow[i] = (int8_t)q8(out_at(i, src.load1(i)), inv);
+    for (int i = H; i < a.ldq; i++) qrow[i] = 0;
+    a.sa[r] = s;
+  }
+}
+
+// One wave per row: quantizeA on rows of f32 (no LayerNorm).
+__global__ __launch_bounds__(256) void quant_rows_kernel(const float *x, int ld, int M, int K,
+                                                         int8_t *q, int ldq, float *sa) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= M) return;
+  const float *row = x + (size_t)r * ld;
+  float mx = 0.f;
+  for (int i = 4 * lane; i < K; i += 256) {
+    const float4 v = *(const float4 *)(row + i);
+    mx = fmax32(mx, fmax32(fmax32(fabsf(v.x), fabsf(v.y)), fmax32(fabsf(v.z), fabsf(v.w))));
+  }
+  for (int t = 1; t < 64; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t));
+  float s = 0.f, inv = 0.f;
+  if (mx != 0.f) {
+    s = mx / 127.0f;
+    inv = 1.0f / s;
+  }
+  int8_t *qrow = q + (size_t)r * ldq;
+  for (int i = 4 * lane; i < K; i += 256) {
+    const float4 v = *(const float4 *)(row + i);
+    const int q0 = q8(v.x, inv), q1 = q8(v.y, inv), q2 = q8(v.z, inv), q3 = q8(v.w, inv);
+    *(int *)(qrow + i) = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+  }
+  for (int i = K + lane; i < ldq; i += 64) qrow[i] = 0;
+  if (lane == 0) sa[r] = s;
+}
+
+__global__ void positions_kernel(const int32_t *offs, const int32_t *padoff, int32_t *pos,
+                                 int32_t *slot) {
+  const int b = blockIdx.x;
+  const int o = offs[b], n = offs[b + 1] - o, p = padoff[b];
+  for (int t = threadIdx.x; t < n; t += blockDim.x) {
+    pos[o + t] = t;
+    if (slot) slot[o + t] = p + t;
+  }
+}
+
+// infer.go:265-287: float64 sum over the sequence, in token order.
+__global__ void pool_kernel(const float *xn, const int32_t *offs, int H, int cls, float *out) {
+  const int b = blockIdx.y;
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= H) return;
+  const int o = offs[b], n = offs[b + 1] - o;
+  float *dst = out + (size_t)b * H + k;
+  if (n == 0) {
+    *dst = 0.f;
+    return;
+  }
+  if (cls) {
+    *dst = xn[(size_t)o * H + k];
+    return;
+  }
+  double acc = 0.0;
+  for (int t = 0; t < n; t++) acc += (double)xn[(size_t)(o + t) * H + k];
+  *dst = (float)(acc / (double)n);
+}
+
+// heads.go:63-74: z = sum f64(w)*f64(x), in order, + f64(b).
+__global__ void head_logits_kernel(const float *x, int T, int H, const float *w, const float *b,
+                                   int rows, double *z) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= T * rows) return;
+  const int t = g / rows, r = g % rows;
+  const float *xr = x + (size_t)t * H;
+  const float *wr = w + (size_t)r * H;
+  double s = 0.0;
+  for (int i = 0; i < H; i++) s += (double)wr[i] * (double)xr[i];
+  z[g] = s + (double)b[r];
+}
+
+}  // namespace
+
+void launch_rownorm(const RowArgs &a, hipStream_t s) {
+  if (a.M <= 0) return;
+  const int tpr = a.lanes <= 0 ? 1 : a.lanes / 4;
+  const long threads = (long)a.M * tpr;
+  dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+  switch (tpr) {
+  case 1: rownorm_kernel<1><<<grid, block, 0, s>>>(a); break;
+  case 2: rownorm_kernel<2><<<grid, block, 0, s>>>(a); break;
+  case 4: rownorm_kernel<4><<<grid, block, 0, s>>>(a); break;
+  }
+}
+
+void launch_quant_rows(const float *x, int ld, int M, int K, int8_t *q, int ldq, float *sa,
+                       hipStream_t s) {
+  if (M <= 0) return;
+  quant_rows_kernel<<<(M + 3) / 4, 256, 0, s>>>(x, ld, M, K, q, ldq, sa);
+}
+
+void launch_positions(const int32_t *offs, const int32_t *padoff, int B, int32_t *pos,
+                      int32_t *slot, hipStream_t s) {
+  if (B <= 0) return;
+  positions_kernel<<<B, 256, 0, s>>>(offs, padoff, pos, slot);
+}
+
+void launch_pool(const float *xn, const int32_t *offs, int B, int H, int cls, float *out,
+                 hipStream_t s) {
+  if (B <= 0) return;
+  dim3 grid((H + 255) / 256, B);
+  pool_kernel<<<grid, 256, 0, s>>>(xn, offs, H, cls, out);
+}
+
+void launch_head_logits(const float *x, int T, int H, const float *w, const float *b, int rows,
+                        double *z, hipStream_t s) {
+  const long n = (long)T * rows;
+  if (n <= 0) return;
+  head_logits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(x, T, H, w, b, rows, z);
+}
+
+}  // namespace ixh

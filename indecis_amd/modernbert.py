@@ -1,0 +1,290 @@
+"""Host-side mirror of indecis's internal/modernbert inference API, backed by
+the gfx950 library through its C ABI (include/indecis_hip.h).
+
+Config mirrors modernbert.Config (internal/modernbert/model.go:26-80);
+Model.encode_seqs / encode_tokens / encode mirror EncodeSeqs / EncodeTokens
+/ Encode (infer.go:244-299) with the same argument meaning and the same
+errors ("modernbert: id N out of vocabulary", "modernbert: inconsistent
+batch"). Weights holds a model's int8 matrices as PackB8 leaves them
+(int8.go:38-77); Weights.random builds the seeded random-init models the
+parity tests and the benchmark use.
+"""
+import ctypes as C
+import dataclasses
+import json
+
+import numpy as np
+
+from . import _lib
+
+EMB_F32, EMB_BF16, EMB_I8 = 0, 1, 2
+
+
+@dataclasses.dataclass
+class Config:
+    """modernbert.Config (model.go:26-49)."""
+    hidden: int
+    layers: int
+    heads: int
+    intermediate: int
+    vocab: int
+    norm_eps: float = 1e-5
+    global_every: int = 3
+    local_attention: int = 128
+    global_theta: float = 160000.0
+    local_theta: float = 10000.0
+    pooling: str = "mean"
+    pad_id: int = 0
+    activation: str = "gelu"
+
+    def head_dim(self):
+        return self.hidden // self.heads
+
+    def is_global(self, layer):
+        """IsGlobal (model.go:59)."""
+        return layer % self.global_every == 0
+
+    def window(self):
+        """Window (model.go:62): half of the local attention width."""
+        return self.local_attention // 2
+
+    def cls(self):
+        return self.pooling == "cls"
+
+    def validate(self):
+        """validate (model.go:64-80)."""
+        if min(self.hidden, self.layers, self.heads, self.intermediate, self.vocab) <= 0:
+            raise ValueError("modernbert: invalid dimensions")
+        if self.hidden % self.heads != 0 or self.head_dim() % 2 != 0:
+            raise ValueError(f"modernbert: hidden_size {self.hidden} incompatible with {self.heads} heads")
+        if self.global_every <= 0 or self.local_attention <= 0:
+            raise ValueError("modernbert: invalid attention windows")
+        if self.activation != "gelu":
+            raise ValueError(f'modernbert: activation "{self.activation}" not supported')
+        if self.pooling not in ("", "mean", "cls"):
+            raise ValueError(f'modernbert: pooling "{self.pooling}" not supported')
+
+    @classmethod
+    def from_json(cls, text):
+        """config.json fields read by Load (model.go:124-144)."""
+        d = json.loads(text)
+        if d.get("attention_bias") or d.get("mlp_bias") or d.get("norm_bias"):
+            raise ValueError("modernbert: biases are not supported")
+        return cls(hidden=d["hidden_size"], layers=d["num_hidden_layers"],
+                   heads=d["num_attention_heads"], intermediate=d["intermediate_size"],
+                   vocab=d["vocab_size"], norm_eps=d.get("norm_eps", 1e-5),
+                   global_every=d["global_attn_every_n_layers"],
+                   local_attention=d["local_attention"],
+                   global_theta=d.get("global_rope_theta", 160000.0),
+                   local_theta=d.get("local_rope_theta", 10000.0),
+                   pooling=d.get("classifier_pooling", "") or "mean",
+                   pad_id=d.get("pad_token_id", 0),
+                   activation=d.get("hidden_activation", "gelu"))
+
+
+# The BASELINE.json shapes.
+SMALL = Config(hidden=256, layers=6, heads=4, intermediate=512, vocab=32768)
+BASE = Config(hidden=768, layers=22, heads=12, intermediate=1152, vocab=50368)
+
+
+def pack_b8(w, transB=True):
+    """PackB8 (linalg/int8.go:38-77) of op(B) k x n: per output channel j,
+    s = max|w|/127 (float32), q = math.Round(float64(float32(w/s))) (half
+    away from zero). Returns q [n][k] int8, scale [n] float32."""
+    w = np.asarray(w, np.float32)
+    wt = w if transB else w.T          # [n][k]
+    mx = np.abs(wt).max(axis=1)
+    s = (mx / np.float32(127)).astype(np.float32)
+    safe = np.where(s == 0, np.float32(1), s).astype(np.float32)
+    x = (wt / safe[:, None]).astype(np.float32).astype(np.float64)
+    q = np.trunc(x + np.copysign(0.5, x))
+    q = np.where(s[:, None] == 0, 0, q).astype(np.int8)
+    return np.ascontiguousarray(q), np.where(mx == 0, np.float32(0), s).astype(np.float32)
+
+
+class Weights:
+    """The tensors a model needs on the int8 path, layer-major:
+    wqkv_q [L][3H][H], wo_q [L][H][H], wi_q [L][2I][H] (GELU-input rows then
+    gate rows, model.go:96), womlp_q [L][H][I] int8 with one float32 scale
+    per output channel; LayerNorm weights; the embedding table."""
+
+    def __init__(self, cfg, rope_rows=512):
+        self.cfg = cfg
+        self.rope_rows = rope_rows
+        self.emb_format = EMB_F32
+        self.emb_f32 = None
+        self.emb_bf16 = None
+        self.emb_exact_ids = np.zeros(0, np.int32)
+        self.emb_exact_rows = np.zeros((0, cfg.hidden), np.float32)
+        self.emb_i8 = None
+        self.emb_i8_scale = None
+
+    @staticmethod
+    def random(cfg, seed=0, emb_format=EMB_F32, weight_scale=(2e-4, 6e-4), n_exact=8):
+        """Seeded random-init model: int8 weights U[-127, 127] with scales
+        U(weight_scale) (an effective std of about 0.015-0.045), LayerNorm
+        weights U(0.9, 1.1), embeddings N(0, 1) in the requested format."""
+        rng = np.random.default_rng(seed)
+        H, I, L, V = cfg.hidden, cfg.intermediate, cfg.layers, cfg.vocab
+        w = Weights(cfg)
+
+        def mat(n, k):
+            q = rng.integers(-127, 128, size=(L, n, k), dtype=np.int8)
+            s = rng.uniform(*weight_scale, size=(L, n)).astype(np.float32)
+            return q, s
+
+        w.wqkv_q, w.wqkv_s = mat(3 * H, H)
+        w.wo_q, w.wo_s = mat(H, H)
+        w.wi_q, w.wi_s = mat(2 * I, H)
+        w.womlp_q, w.womlp_s = mat(H, I)
+        w.attn_norm = rng.uniform(0.9, 1.1, size=(L, H)).astype(np.float32)
+        w.mlp_norm = rng.uniform(0.9, 1.1, size=(L, H)).astype(np.float32)
+        w.emb_norm = rng.uniform(0.9, 1.1, size=H).astype(np.float32)
+        w.final_norm = rng.uniform(0.9, 1.1, size=H).astype(np.float32)
+        emb = rng.standard_normal((V, H), dtype=np.float32)
+        w.set_embeddings(emb, emb_format, rng=rng, n_exact=n_exact)
+        return w
+
+    def set_embeddings(self, emb, fmt, rng=None, n_exact=8):
+        """Stores a float32 table in one of the three formats the reference
+        reads (embeddings.go:24-68): float32; bf16 (truncated) plus n_exact
+        float32 rows that override their ids; int8 with a scale per row."""
+        emb = np.ascontiguousarray(emb, np.float32)
+        self.emb_format = fmt
+        if fmt == EMB_F32:
+            self.emb_f32 = emb
+        elif fmt == EMB_BF16:
+            self.emb_bf16 = (emb.view(np.uint32) >> 16).astype(np.uint16)
+            rng = rng or np.random.default_rng(0)
+            ids = rng.choice(emb.shape[0], size=min(n_exact, emb.shape[0]), replace=False)
+            self.emb_exact_ids = np.sort(ids).astype(np.int32)
+            self.emb_exact_rows = emb[self.emb_exact_ids] * np.float32(1.25)
+        elif fmt == EMB_I8:
+            mx = np.abs(emb).max(axis=1)
+            s = (mx / np.float32(127)).astype(np.float32)
+            safe = np.where(s == 0, np.float32(1), s)
+            self.emb_i8 = np.clip(np.rint(emb / safe[:, None]), -127, 127).astype(np.int8)
+            self.emb_i8_scale = s
+        else:
+            raise ValueError(f"embedding format {fmt}")
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _offsets(seqs):
+    offs = np.zeros(len(seqs) + 1, np.int32)
+    if seqs:
+        offs[1:] = np.cumsum([len(s) for s in seqs])
+    ids = (np.concatenate([np.asarray(s, np.int32) for s in seqs])
+           if seqs and offs[-1] > 0 else np.zeros(1, np.int32))
+    return np.ascontiguousarray(ids, np.int32), offs
+
+
+class Model:
+    """modernbert.Model on the int8 path, its weights resident on one GPU."""
+
+    def __init__(self, weights, device=0, lanes=8):
+        self.cfg = cfg = weights.cfg
+        cfg.validate()
+        self.lanes = lanes
+        L = _lib.lib()
+        c = _lib.IxhConfig(
+            hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads,
+            intermediate=cfg.intermediate, vocab=cfg.vocab, norm_eps=cfg.norm_eps,
+            global_every=cfg.global_every, local_attention=cfg.local_attention,
+            global_theta=cfg.global_theta, local_theta=cfg.local_theta,
+            pooling=_lib.POOL_CLS if cfg.cls() else _lib.POOL_MEAN, lanes=lanes)
+        h = C.c_void_p()
+        _lib.check(L.ixh_model_create(C.byref(c), device, C.byref(h)))
+        self._h = h
+        self._L = L
+        self.device = device
+        self.upload(weights)
+
+    def upload(self, w):
+        """packs() (infer.go:184-219): uploads every matrix and table."""
+        L, h, cfg = self._L, self._h, self.cfg
+        for l in range(cfg.layers):
+            for which, q, s in ((_lib.MAT_QKV, w.wqkv_q, w.wqkv_s), (_lib.MAT_O, w.wo_q, w.wo_s),
+                                (_lib.MAT_I, w.wi_q, w.wi_s), (_lib.MAT_OMLP, w.womlp_q, w.womlp_s)):
+                qa = np.ascontiguousarray(q[l], np.int8)
+                sa = np.ascontiguousarray(s[l], np.float32)
+                _lib.check(L.ixh_model_set_matrix(h, l, which, _ptr(qa), _ptr(sa), _lib.LAYOUT_ROWS))
+            if l > 0:
+                g = np.ascontiguousarray(w.attn_norm[l], np.float32)
+                _lib.check(L.ixh_model_set_norm(h, _lib.NORM_ATTN, l, _ptr(g)))
+            g = np.ascontiguousarray(w.mlp_norm[l], np.float32)
+            _lib.check(L.ixh_model_set_norm(h, _lib.NORM_MLP, l, _ptr(g)))
+        for which, g in ((_lib.NORM_EMB, w.emb_norm), (_lib.NORM_FINAL, w.final_norm)):
+            g = np.ascontiguousarray(g, np.float32)
+            _lib.check(L.ixh_model_set_norm(h, which, 0, _ptr(g)))
+        if w.emb_format == EMB_F32:
+            _lib.check(L.ixh_model_set_embeddings_f32(h, _ptr(w.emb_f32)))
+        elif w.emb_format == EMB_BF16:
+            ids = np.ascontiguousarray(w.emb_exact_ids, np.int32)
+            rows = np.ascontiguousarray(w.emb_exact_rows, np.float32)
+            _lib.check(L.ixh_model_set_embeddings_bf16(h, _ptr(w.emb_bf16), _ptr(ids), _ptr(rows), len(ids)))
+        else:
+            _lib.check(L.ixh_model_set_embeddings_i8(h, _ptr(w.emb_i8), _ptr(w.emb_i8_scale)))
+
+    def set_rope(self, is_global, cos_t, sin_t):
+        """Go's ropeFor tables (model.go:256-277), [rows][D/2]."""
+        c = np.ascontiguousarray(cos_t, np.float32)
+        s = np.ascontiguousarray(sin_t, np.float32)
+        _lib.check(self._L.ixh_model_set_rope(self._h, 1 if is_global else 0, _ptr(c), _ptr(s), c.shape[0]))
+
+    def invalidate(self):
+        """Invalidate (infer.go:95-100)."""
+        _lib.check(self._L.ixh_model_invalidate(self._h))
+
+    def encode_seqs(self, seqs):
+        """EncodeSeqs (infer.go:261-289): [B, H] pooled embeddings."""
+        ids, offs = _offsets(seqs)
+        out = np.zeros((max(len(seqs), 1), self.cfg.hidden), np.float32)
+        _lib.check(self._L.ixh_encode_seqs(self._h, _ptr(ids), _ptr(offs), len(seqs), _ptr(out)))
+        return out[:len(seqs)]
+
+    def encode_tokens(self, seqs):
+        """EncodeTokens (infer.go:293-299): [sum of lengths, H]."""
+        ids, offs = _offsets(seqs)
+        N = int(offs[-1])
+        out = np.zeros((max(N, 1), self.cfg.hidden), np.float32)
+        _lib.check(self._L.ixh_encode_tokens(self._h, _ptr(ids), _ptr(offs), len(seqs), _ptr(out)))
+        return out[:N]
+
+    def encode(self, ids, lens, T):
+        """Encode (infer.go:244-253): a batch right-padded to T tokens
+        (IDs [B*T], Lens [B]); padding never reaches the GPU."""
+        ids = np.asarray(ids, np.int32)
+        if ids.size != len(lens) * T:
+            raise ValueError("modernbert: inconsistent batch")
+        return self.encode_seqs([ids[i * T:i * T + n] for i, n in enumerate(lens)])
+
+    def encode_device(self, ids_ptr, offs, out_ptr, kind=_lib.OUT_POOLED, stream=None):
+        """ixh_encode_device: ids and out are device pointers (ints)."""
+        offs = np.ascontiguousarray(offs, np.int32)
+        _lib.check(self._L.ixh_encode_device(self._h, C.c_void_p(ids_ptr), _ptr(offs), len(offs) - 1,
+                                             kind, C.c_void_p(out_ptr),
+                                             C.c_void_p(stream) if stream else None))
+
+    def head_logits(self, x, w, b):
+        """head.logits (heads.go:63-74) of rows x: [T, rows] float64."""
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        z = np.zeros((max(x.shape[0], 1), w.shape[0]), np.float64)
+        _lib.check(self._L.ixh_head_logits(self._h, _ptr(x), x.shape[0], _ptr(w), _ptr(b), w.shape[0], _ptr(z)))
+        return z[:x.shape[0]]
+
+    def close(self):
+        if self._h:
+            self._L.ixh_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

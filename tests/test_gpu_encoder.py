@@ -1,0 +1,176 @@
+"""GPU parity of the whole int8 encoder (modernbert.run, infer.go:304-430)
+against the CPU oracle, through the C ABI, on the BASELINE.json
+configurations (reduced batches where the oracle would take minutes), plus
+the reference's invariants at full size."""
+import concurrent.futures as cf
+
+import numpy as np
+import pytest
+
+from helpers import (base_cfg, f32_bits_equal, ids_cfg2, ids_uniform_lengths, mismatch_report,
+                     small_cfg)
+from indecis_amd import _lib, heads
+from indecis_amd.modernbert import EMB_BF16, EMB_F32, EMB_I8, Model, Weights
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+_models = {}
+
+
+def model_pair(cfg, seed=0, emb_format=EMB_F32, lanes=8):
+    key = (tuple(cfg.__dict__.values()), seed, emb_format, lanes)
+    if key not in _models:
+        w = Weights.random(cfg, seed=seed, emb_format=emb_format)
+        _models[key] = (w, Model(w, lanes=lanes), orc.OracleModel(w, lanes=lanes))
+    return _models[key]
+
+
+def test_cfg2_pooled_and_heads():
+    """cfg2: small encoder, 64 x 15 tokens, mean pooling, an 8-way choice
+    head and a yes/no head."""
+    cfg = small_cfg()
+    w, gpu, ora = model_pair(cfg)
+    rng = np.random.default_rng(2)
+    seqs = ids_cfg2(rng)
+    got = gpu.encode_seqs(seqs)
+    want = ora.encode_seqs(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+    hw, hb = heads.random_head(8, cfg.hidden, rng)
+    nw, nb = heads.random_head(1, cfg.hidden, rng)
+    z = gpu.head_logits(got, hw, hb)
+    zr = orc.head_logits(want, hw, hb)
+    assert np.array_equal(z, zr)
+    p = heads.softmax(z)
+    assert np.allclose(p.sum(axis=1), 1.0)
+    zn = gpu.head_logits(got, nw, nb)
+    assert np.array_equal(zn, orc.head_logits(want, nw, nb))
+
+
+def test_cfg3_tokens_and_spans():
+    """cfg3 (reduced batch): lengths U[16,256], token states and a 9-label
+    spans head on every token; the padded Encode form equals EncodeSeqs."""
+    cfg = small_cfg()
+    w, gpu, ora = model_pair(cfg)
+    rng = np.random.default_rng(3)
+    seqs = ids_uniform_lengths(rng, 24, 16, 256, cfg.vocab)
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+    sw, sb = heads.random_head(heads.span_tag_count(4), cfg.hidden, rng)
+    assert np.array_equal(gpu.head_logits(got, sw, sb), orc.head_logits(want, sw, sb))
+    T = 256
+    ids = np.zeros(len(seqs) * T, np.int32)
+    for i, s in enumerate(seqs):
+        ids[i * T:i * T + len(s)] = s
+    pooled = gpu.encode(ids, [len(s) for s in seqs], T)
+    assert f32_bits_equal(pooled, ora.encode_seqs(seqs))
+
+
+@pytest.mark.parametrize("emb_format", [EMB_BF16, EMB_I8])
+def test_embedding_formats(emb_format):
+    cfg = small_cfg(layers=2)
+    w, gpu, ora = model_pair(cfg, seed=5, emb_format=emb_format)
+    rng = np.random.default_rng(4)
+    seqs = ids_uniform_lengths(rng, 6, 1, 40, cfg.vocab)
+    if emb_format == EMB_BF16:
+        seqs.append(np.asarray(w.emb_exact_ids, np.int32))  # exact rows used
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+
+
+@pytest.mark.parametrize("lanes", [0, 4, 16])
+def test_lanes_variants(lanes):
+    cfg = small_cfg(layers=3)
+    w, gpu, ora = model_pair(cfg, seed=6, lanes=lanes)
+    rng = np.random.default_rng(lanes + 10)
+    seqs = ids_uniform_lengths(rng, 5, 1, 200, cfg.vocab)
+    got = gpu.encode_seqs(seqs)
+    want = ora.encode_seqs(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+
+
+def test_base_shape_exact():
+    """The ModernBERT-base shape of cfg4 (H 768, 22 layers, 12 heads, I 1152)
+    on a few sequences of lengths U[64, 512]."""
+    cfg = base_cfg()
+    w, gpu, ora = model_pair(cfg, seed=7)
+    rng = np.random.default_rng(8)
+    seqs = ids_uniform_lengths(rng, 3, 64, 512, cfg.vocab)
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+
+
+def test_long_context_exact():
+    """cfg5-style long sequence (global attention over 2,100 keys, local
+    window elsewhere), base width with 4 layers (global, local, local,
+    global)."""
+    cfg = base_cfg(layers=4)
+    w, gpu, ora = model_pair(cfg, seed=9)
+    rng = np.random.default_rng(10)
+    seqs = [rng.integers(0, cfg.vocab, size=2100, dtype=np.int32),
+            rng.integers(0, cfg.vocab, size=333, dtype=np.int32)]
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+
+
+def test_batch_equals_single():
+    """A sequence's states do not depend on its batch (forward_test.go:141-160,
+    TestMatMul8RowsIndependent)."""
+    cfg = small_cfg()
+    w, gpu, _ = model_pair(cfg)
+    rng = np.random.default_rng(11)
+    seqs = ids_uniform_lengths(rng, 40, 1, 300, cfg.vocab)
+    allt = gpu.encode_tokens(seqs)
+    off = 0
+    for s in seqs[:8]:
+        one = gpu.encode_tokens([s])
+        assert f32_bits_equal(one, allt[off:off + len(s)])
+        off += len(s)
+
+
+def test_errors_and_empty():
+    cfg = small_cfg(layers=1)
+    w, gpu, _ = model_pair(cfg)
+    with pytest.raises(_lib.IxhError, match="modernbert: id 40000 out of vocabulary"):
+        gpu.encode_seqs([np.array([1, 40000, 2], np.int32)])
+    with pytest.raises(_lib.IxhError, match="modernbert: id -1 out of vocabulary"):
+        gpu.encode_seqs([np.array([-1], np.int32)])
+    with pytest.raises(ValueError, match="inconsistent batch"):
+        gpu.encode(np.zeros(5, np.int32), [2, 2], 2)
+    out = gpu.encode_seqs([np.zeros(0, np.int32), np.array([3, 4], np.int32)])
+    assert np.all(out[0] == 0) and np.any(out[1] != 0)
+    assert gpu.encode_seqs([]).shape == (0, cfg.hidden)
+    assert gpu.encode_tokens([np.zeros(0, np.int32)]).shape == (0, cfg.hidden)
+
+
+def test_concurrent_inference():
+    """TestConcurrentInference (concurrency_test.go:12-70): 8 threads on one
+    model give the sequential results."""
+    cfg = small_cfg(layers=2)
+    w, gpu, _ = model_pair(cfg)
+    rng = np.random.default_rng(12)
+    batches = [ids_uniform_lengths(rng, 4, 1, 120, cfg.vocab) for _ in range(16)]
+    want = [gpu.encode_seqs(b) for b in batches]
+    with cf.ThreadPoolExecutor(8) as ex:
+        got = list(ex.map(gpu.encode_seqs, batches))
+    for g, wnt in zip(got, want):
+        assert f32_bits_equal(g, wnt)
+
+
+def test_invalidate_requires_upload():
+    cfg = small_cfg(layers=1)
+    w = Weights.random(cfg, seed=13)
+    m = Model(w)
+    seq = [np.array([5, 6, 7], np.int32)]
+    before = m.encode_seqs(seq)
+    m.invalidate()
+    with pytest.raises(_lib.IxhError) as e:
+        m.encode_seqs(seq)
+    assert e.value.code == _lib.IXH_ESTATE
+    m.upload(w)
+    assert f32_bits_equal(m.encode_seqs(seq), before)
+    m.close()

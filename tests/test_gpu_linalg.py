@@ -1,0 +1,128 @@
+"""GPU parity of the linalg-level kernels against the CPU oracle, through
+the C ABI: quantised activations and int32 accumulators bit-exact, float
+outputs bit-exact (the kernels reproduce the reference's roundings)."""
+import numpy as np
+import pytest
+
+from helpers import f32_bits_equal, mismatch_report
+from indecis_amd import linalg
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(rng, n, k, kind="random"):
+    if kind == "max":
+        q = np.full((n, k), 127, np.int8)
+    elif kind == "mixed":
+        q = np.where((np.arange(n * k).reshape(n, k) // 3) % 2 == 0, -127, 127).astype(np.int8)
+    else:
+        q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+    return q, s
+
+
+def test_cfg1_fused_op():
+    """BASELINE cfg1: X [256x256] N(0,1), gamma U(0.9,1.1), LN eps 1e-5,
+    per-row quantisation, W int8 [256 x 1024] U[-127,127], scales
+    U(1e-3,1e-2), dequant + GeGLU (GELU on the first 512, infer.go:418)."""
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((256, 256)).astype(np.float32)
+    gamma = rng.uniform(0.9, 1.1, 256).astype(np.float32)
+    q, s = _weights(rng, 1024, 256)
+    b = linalg.PackedB8(q, s)
+    for lanes in (8, 16, 0):
+        xn_ref = orc.layernorm_rows(x, gamma, 1e-5, lanes)
+        aq_ref, sa_ref = orc.quantize_rows(xn_ref)
+        tile_ref = orc.matmul8_tile(aq_ref, q)
+        colsum = q.astype(np.int32).sum(axis=1).astype(np.int32)
+        z_ref = orc.matmul8_deq(aq_ref, sa_ref, q, s, colsum)
+        g_ref = orc.gelu_mul(z_ref[:, :512], z_ref[:, 512:], lanes)
+        out, aq, sa = linalg.layernorm_quant(x, gamma, 1e-5, lanes)
+        assert f32_bits_equal(out, xn_ref), mismatch_report(out, xn_ref)
+        assert np.array_equal(aq, aq_ref)
+        assert f32_bits_equal(sa, sa_ref)
+        g, tile = linalg.ln_matmul8_geglu(x, gamma, b, 1e-5, lanes)
+        assert np.array_equal(tile, tile_ref)
+        assert f32_bits_equal(g, g_ref), mismatch_report(g, g_ref)
+
+
+@pytest.mark.parametrize("kind", ["random", "max", "mixed"])
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (6, 4, 16), (7, 384, 1152), (15, 1152, 384),
+                                   (33, 301, 17), (130, 768, 2304), (257, 70, 40)])
+def test_matmul8_tile_exact(m, k, n, kind):
+    """microKernel8 == microKernel8Go (kernel_test.go:76-95): the GPU's
+    reference tile and quantised activations equal the oracle's."""
+    rng = np.random.default_rng(m * 7919 + k * 31 + n)
+    a = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    if kind == "max":
+        a[:] = np.abs(a) + 1
+    q, s = _weights(rng, n, k, kind)
+    b = linalg.PackedB8(q, s)
+    aq, sa, tile = linalg.matmul8_tile(a, b)
+    aq_ref, sa_ref = orc.quantize_rows(a)
+    assert np.array_equal(aq, aq_ref)
+    assert f32_bits_equal(sa, sa_ref)
+    assert np.array_equal(tile, orc.matmul8_tile(aq_ref, q))
+
+
+@pytest.mark.parametrize("accumulate", [False, True])
+@pytest.mark.parametrize("m,k,n", [(1, 64, 128), (13, 70, 40), (100, 768, 768), (300, 1152, 768)])
+def test_matmul8_float_exact(m, k, n, accumulate):
+    """MatMul8N: c (+)= ((f32(tile) - zc)*sb)*sa bit for bit."""
+    rng = np.random.default_rng(m + k + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    a[min(2, m - 1)] = 0.0  # a zero row: scale 0
+    q, s = _weights(rng, n, k)
+    b = linalg.PackedB8(q, s)
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    colsum = q.astype(np.int32).sum(axis=1).astype(np.int32)
+    ref = orc.matmul8(a, q, s, colsum, c=c0, accumulate=accumulate)
+    c = c0.copy()
+    linalg.matmul8(c, a, b, m, accumulate)
+    assert f32_bits_equal(c, ref), mismatch_report(c, ref)
+
+
+def test_matmul8_rows_independent():
+    """TestMatMul8RowsIndependent (int8_test.go:149-171)."""
+    rng = np.random.default_rng(3)
+    m, k, n = 13, 70, 40
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    q, s = _weights(rng, n, k)
+    b = linalg.PackedB8(q, s)
+    allc = np.zeros((m, n), np.float32)
+    linalg.matmul8(allc, a, b, m)
+    for i in range(m):
+        one = np.zeros((1, n), np.float32)
+        linalg.matmul8(one, a[i:i + 1].copy(), b, 1)
+        assert f32_bits_equal(one[0], allc[i])
+
+
+@pytest.mark.parametrize("lanes", [0, 4, 8, 16])
+@pytest.mark.parametrize("m,h", [(1, 4), (7, 36), (64, 256), (300, 768), (5, 1152)])
+def test_layernorm_quant_exact(m, h, lanes):
+    rng = np.random.default_rng(m * h + lanes)
+    x = (rng.standard_normal((m, h)) * 3 + 0.5).astype(np.float32)
+    gamma = rng.uniform(0.9, 1.1, h).astype(np.float32)
+    ref = orc.layernorm_rows(x, gamma, 1e-5, lanes)
+    q_ref, sa_ref = orc.quantize_rows(ref)
+    out, q, sa = linalg.layernorm_quant(x, gamma, 1e-5, lanes)
+    assert f32_bits_equal(out, ref), mismatch_report(out, ref)
+    assert np.array_equal(q, q_ref)
+    assert f32_bits_equal(sa, sa_ref)
+
+
+@pytest.mark.parametrize("lanes", [8, 16, 0])
+@pytest.mark.parametrize("window", [-1, 8, 64])
+@pytest.mark.parametrize("n", [1, 5, 17, 48, 100, 259, 300, 600])
+def test_attend8_exact(n, window, lanes):
+    """Attend8 on the GPU == the oracle's restatement, bit for bit, with the
+    inputs of TestAttend8 (attention8_test.go:50-68)."""
+    rng = np.random.default_rng(n * 100 + window + 7 * lanes)
+    D = 64
+    q = (rng.standard_normal((n, D)) * 2).astype(np.float32)
+    k = (rng.standard_normal((n, D)) * 2).astype(np.float32) + (np.arange(n * D) % D % 7).reshape(n, D).astype(np.float32)
+    v = rng.standard_normal((n, D)).astype(np.float32)
+    ref = orc.attend8(q, k, v, window, 0.125, lanes)
+    o = linalg.attend8(q, k, v, window, 0.125, lanes)
+    assert f32_bits_equal(o, ref), mismatch_report(o, ref)
