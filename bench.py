@@ -1,0 +1,215 @@
+"""Headline benchmark: encoder tokens/s of indecis's int8 ModernBERT-base
+forward pass ("cfg4") on one MI355X, plus the
+fraction of the int8 MFMA peak its kernels reach.
+
+A step is one EncodeSeqs pass over the whole batch: 256 sequences with
+lengths uniform in [64, 512] (seeded), ids uniform over the 50,368-token
+vocabulary, packed end to end by cumulative offsets, random-init int8
+weights of the ModernBERT-base shape (H 768, 22 layers, 12 heads, GeGLU
+2x1152). The ids are already in HBM when the timed region starts and the
+pooled [256, 768] output stays there (ixh_encode_device).
+
+Prints one JSON line. `roofline` is for the kernel class with the most GPU
+time, from HIP events recorded around every launch during the timed steps
+(algorithmic int8 ops or HBM bytes per launch over the average launch
+duration); `traffic` comes from a committed rocprofv3 PMC summary of that
+kernel (profiles/pmc_<kernel>.json) when one matches, else null.
+`cpu_baseline` times the C restatement of the reference (oracle/, test
+infrastructure) on a bounded sample of the same batch on the host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_INT8_OPS = 5.0e15   # MI355X dense int8 MFMA, ops/s
+PEAK_HBM = 8.0e12        # MI355X HBM3E, bytes/s
+
+WORKLOADS = {
+    # name: (model, batch, min length, max length)
+    "cfg4": ("base", 256, 64, 512),
+    "cfg3": ("small", 256, 16, 256),
+    "cfg5": ("base", 8, 8192, 8192),
+}
+
+
+def make_inputs(np, vocab, B, lo, hi, seed=20261201):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(lo, hi + 1, size=B)
+    seqs = [rng.integers(0, vocab, size=int(n), dtype=np.int32) for n in lens]
+    return seqs
+
+
+def cpu_baseline(np, weights, seqs, max_tokens):
+    """Times the oracle (C restatement of the reference int8 path, OpenMP)
+    on the first sequences of the batch, up to max_tokens tokens."""
+    from oracle import oracle as orc
+    sample, n = [], 0
+    for s in seqs:
+        if n + len(s) > max_tokens and sample:
+            break
+        sample.append(s)
+        n += len(s)
+    om = orc.OracleModel(weights, lanes=8)
+    om.encode_seqs(sample[:1])  # warm-up
+    t0 = time.perf_counter()
+    om.encode_seqs(sample)
+    dt = time.perf_counter() - t0
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(n / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"first {len(sample)} sequences ({n} tokens) of the same batch, "
+                      f"{dt:.1f} s, C restatement of linalg/modernbert int8 (OpenMP), not the Go reference"}
+
+
+def load_traffic(kernel, workload):
+    path = os.path.join(ROOT, "profiles", f"pmc_{kernel}.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        d = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    if d.get("workload") != workload or d.get("kernel_class") != kernel:
+        return None
+    return d.get("hbm_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="cfg4", choices=sorted(WORKLOADS))
+    ap.add_argument("--lanes", type=int, default=8)
+    ap.add_argument("--cpu-tokens", type=int, default=4096,
+                    help="tokens of the batch timed on the CPU baseline (0: skip)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run one device copy of 512 MiB (PMC calibration)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {max(args.gpus, world)}); "
+              "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from indecis_amd import _lib
+    from indecis_amd.modernbert import BASE, SMALL, Model, Weights
+
+    mname, B, lo, hi = WORKLOADS[args.workload]
+    cfg = BASE if mname == "base" else SMALL
+    weights = Weights.random(cfg, seed=4)
+    seqs = make_inputs(np, cfg.vocab, B, lo, hi)
+    offs = np.zeros(B + 1, np.int32)
+    offs[1:] = np.cumsum([len(s) for s in seqs])
+    N = int(offs[-1])
+
+    torch.cuda.set_device(0)
+    model = Model(weights, device=0, lanes=args.lanes)
+    ids_d = torch.from_numpy(np.concatenate(seqs)).to("cuda")
+    out_d = torch.empty((B, cfg.hidden), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        model.encode_device(ids_d.data_ptr(), offs, out_d.data_ptr(), _lib.OUT_POOLED, stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    if args.copy_probe:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    model.set_profiling(True)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    prof = model.profile()
+    model.set_profiling(False)
+    gpu_ms = ev0.elapsed_time(ev1) / args.steps
+    ms_per_step = wall * 1000 / args.steps
+
+    # per-class figures per step and the dominant class
+    kernels = {}
+    for name, s in prof.items():
+        per_launch_ms = s["ms"] / max(s["launches"], 1)
+        if s["ops"] > 0:
+            ach = s["ops"] / (s["ms"] / 1e3) / 1e12
+            kernels[name] = {"ms_per_step": round(s["ms"] / args.steps, 3), "TOP/s": round(ach, 1),
+                             "mfma_frac": round(ach * 1e12 / PEAK_INT8_OPS, 4)}
+        else:
+            ach = s["bytes"] / (s["ms"] / 1e3) / 1e9
+            kernels[name] = {"ms_per_step": round(s["ms"] / args.steps, 3), "GB/s": round(ach, 1),
+                             "hbm_frac": round(ach * 1e9 / PEAK_HBM, 4)}
+        kernels[name]["avg_launch_us"] = round(per_launch_ms * 1e3, 2)
+    dom = max(prof, key=lambda k: prof[k]["ms"])
+    d = prof[dom]
+    avg_s = d["ms"] / d["launches"] / 1e3
+    if d["ops"] > 0:
+        per_launch = d["ops"] / d["launches"]
+        roof = {"bound": "mfma", "achieved": round(per_launch / avg_s / 1e12, 2),
+                "peak": PEAK_INT8_OPS / 1e12, "unit": "TOP/s"}
+    else:
+        per_launch = d["bytes"] / d["launches"]
+        roof = {"bound": "hbm", "achieved": round(per_launch / avg_s / 1e9, 1),
+                "peak": PEAK_HBM / 1e9, "unit": "GB/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = load_traffic(dom, args.workload)
+    roof["kernel"] = dom
+    roof["algorithmic_per_launch"] = per_launch
+    roof["avg_launch_us"] = round(avg_s * 1e6, 2)
+    gemm = [s for n, s in prof.items() if n.startswith("gemm_")]
+    gemm_ops = sum(s["ops"] for s in gemm)
+    gemm_ms = sum(s["ms"] for s in gemm)
+
+    cpu = None
+    if args.cpu_tokens > 0:
+        cpu = cpu_baseline(np, weights, seqs, args.cpu_tokens)
+
+    line = {
+        "metric": "encoder tokens/sec (int8, 512-tok, batch 256) + % of int8 MFMA peak",
+        "value": round(N / (ms_per_step / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "gpu_ms_per_step": round(gpu_ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}: ModernBERT-{mname}-shaped int8 encoder, "
+                               f"batch {B} x U[{lo},{hi}] tokens packed by offsets, random-init",
+                   "tokens_per_step": N, "sequences": B, "hidden": cfg.hidden,
+                   "layers": cfg.layers, "heads": cfg.heads, "intermediate": cfg.intermediate,
+                   "vocab": cfg.vocab, "lanes": args.lanes, "parallelism": "single GPU"},
+        "seqs_per_s": round(B / (ms_per_step / 1e3), 1),
+        "gemm_mfma_frac": round(gemm_ops / (gemm_ms / 1e3) / PEAK_INT8_OPS, 4) if gemm_ms else None,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    model.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -124,6 +124,24 @@ int ixh_encode_tokens(ixh_model *m, const int32_t *ids, const int32_t *offs,
 int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs,
                       int B, int out_kind, float *d_out, void *stream);
 
+/* Per-kernel timing (no counterpart in the reference, whose profiling is Go
+ * pprof around the whole call, tools/infbench/main.go:71-88): when on,
+ * every kernel of an encode is bracketed by HIP events on its stream and
+ * its duration, algorithmic int8 ops (GEMM and attention MFMA work, 2 per
+ * multiply-add) and algorithmic HBM bytes are summed per kernel class.
+ * Turning it on or off clears the sums. */
+typedef struct ixh_kernel_stat {
+  char name[48];    /* kernel class, e.g. "gemm_wi" */
+  int64_t launches;
+  double ms;        /* summed event-measured durations */
+  double ops;       /* summed algorithmic int8 ops */
+  double bytes;     /* summed algorithmic HBM bytes */
+} ixh_kernel_stat;
+int ixh_model_set_profiling(ixh_model *m, int on);
+/* Copies up to cap class records into out; *n receives the number of
+ * classes. */
+int ixh_model_profile(ixh_model *m, ixh_kernel_stat *out, int cap, int *n);
+
 /* head.logits (heads.go:63-74) on host rows: z[t][r] = sum_i
  * f64(w[r][i]) f64(x[t][i]) + f64(b[r]), computed on the model's GPU. */
 int ixh_head_logits(ixh_model *m, const float *x, int T, const float *w,

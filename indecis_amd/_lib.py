@@ -19,6 +19,7 @@ EXPORTS = [
     "ixh_model_invalidate", "ixh_encode_seqs", "ixh_encode_tokens", "ixh_encode_device",
     "ixh_head_logits", "ixh_packb8_create", "ixh_packb8_destroy", "ixh_matmul8",
     "ixh_matmul8_tile", "ixh_layernorm_quant", "ixh_ln_matmul8_geglu", "ixh_attend8",
+    "ixh_model_set_profiling", "ixh_model_profile",
 ]
 
 IXH_OK, IXH_EINVAL, IXH_ERANGE, IXH_ESTATE, IXH_EHIP, IXH_ENOMEM = range(6)
@@ -33,6 +34,11 @@ class IxhError(RuntimeError):
     def __init__(self, code, msg):
         super().__init__(msg)
         self.code = code
+
+
+class IxhKernelStat(C.Structure):
+    _fields_ = [("name", C.c_char * 48), ("launches", C.c_int64), ("ms", C.c_double),
+                ("ops", C.c_double), ("bytes", C.c_double)]
 
 
 class IxhConfig(C.Structure):
@@ -81,6 +87,8 @@ def lib():
         "ixh_layernorm_quant": [C.c_int, vp, C.c_int, C.c_int, vp, C.c_double, C.c_int, vp, vp, vp],
         "ixh_ln_matmul8_geglu": [vp, vp, C.c_int, vp, C.c_double, C.c_int, vp, vp],
         "ixh_attend8": [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int],
+        "ixh_model_set_profiling": [vp, C.c_int],
+        "ixh_model_profile": [vp, C.POINTER(IxhKernelStat), C.c_int, C.POINTER(C.c_int)],
     }
     for name, args in sig.items():
         f = getattr(L, name)

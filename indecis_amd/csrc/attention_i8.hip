@@ -165,6 +165,7 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(AttnArgs a) {
   }
 }
 
+template <bool GLOBAL>
 __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t Ks[CHUNK * KS];
   __shared__ __attribute__((aligned(16))) int8_t Vs[D * VS];
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
   const int slot0 = a.padoff[b];
   const int npad = (n + kKeyPad - 1) / kKeyPad * kKeyPad;
   const int H = a.H, W = a.window;
-  const bool global = W < 0;
+  constexpr bool global = GLOBAL;
 
   // this lane's query
   const int q0 = Q0 + 32 * wave;
@@ -355,7 +356,10 @@ void launch_attn_prologue(const AttnArgs &a, hipStream_t s) {
 void launch_attn_main(const AttnArgs &a, hipStream_t s) {
   if (a.nblocks <= 0) return;
   dim3 grid(a.nblocks, a.nh);
-  attn_main_kernel<<<grid, 256, 0, s>>>(a);
+  if (a.window < 0)
+    attn_main_kernel<true><<<grid, 256, 0, s>>>(a);
+  else
+    attn_main_kernel<false><<<grid, 256, 0, s>>>(a);
 }
 
 }  // namespace ixh

@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
         for (int j = 0; j < 2; j++) {
           if (ncol[j] >= a.n_valid) continue;
           const float v = deq(acc[i][j][r] + c128[j], zc[j], sb[j], sa);
-          if constexpr (EPI == EPI_ACCUM)
+          if constexpr (EPI == EPI_ACCUM || EPI == EPI_ACCUM_MLP)
             row[ncol[j]] = row[ncol[j]] + v;
           else
             row[ncol[j]] = v;
@@ -173,6 +173,7 @@ void launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
   case EPI_TILE: gemm_i8_kernel<EPI_TILE><<<grid, block, 0, s>>>(a); break;
   case EPI_GEGLU: gemm_i8_kernel<EPI_GEGLU><<<grid, block, 0, s>>>(a); break;
   case EPI_ROPE: gemm_i8_kernel<EPI_ROPE><<<grid, block, 0, s>>>(a); break;
+  case EPI_ACCUM_MLP: gemm_i8_kernel<EPI_ACCUM_MLP><<<grid, block, 0, s>>>(a); break;
   }
 }
 

@@ -208,9 +208,17 @@ struct Workspace {
   DevBuf ids, offs, padoff, pos, blocks, x, xn, qkv, xq, sa, qq, sq, kp, ks, vt, vs, ctx, g,
       pooled, flag;
   PinBuf host;
+  std::vector<hipEvent_t> events;  // profiling: begin/end pairs, reused
   ~Workspace() {
+    for (hipEvent_t e : events) (void)hipEventDestroy(e);
     if (stream) (void)hipStreamDestroy(stream);
   }
+};
+
+struct StatAcc {
+  std::string name;
+  int64_t launches = 0;
+  double ms = 0, ops = 0, bytes = 0;
 };
 
 }  // namespace
@@ -235,6 +243,9 @@ struct ixh_model {
   std::mutex pool_mu;
   std::vector<Workspace *> pool;
   std::atomic<bool> weights_valid{true};
+  std::atomic<bool> profiling{false};
+  std::mutex prof_mu;
+  std::vector<StatAcc> stats;
   ~ixh_model() {
     for (Workspace *w : pool) delete w;
   }
@@ -350,6 +361,69 @@ __global__ void check_ids_kernel(const int32_t *ids, int N, int vocab, int *flag
   if (t < N && (ids[t] < 0 || ids[t] >= vocab)) atomicMin(flag, t);
 }
 
+// Brackets launches with HIP events when the model profiles; after the
+// stream is synchronised, flush() adds the durations to the model's sums.
+struct Prof {
+  ixh_model *m;
+  Workspace *w;
+  hipStream_t st;
+  bool on;
+  struct Rec {
+    const char *name;
+    int idx;
+    double ops, bytes;
+  };
+  std::vector<Rec> recs;
+  int used = 0;
+  int err = IXH_OK;
+
+  int begin() {
+    if (!on || err) return -1;
+    if ((int)w->events.size() < 2 * (used + 1)) {
+      hipEvent_t a, b;
+      if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
+        err = fail(IXH_EHIP, "modernbert: hip: event creation failed");
+        return -1;
+      }
+      w->events.push_back(a);
+      w->events.push_back(b);
+    }
+    if (hipEventRecord(w->events[2 * used], st) != hipSuccess) {
+      err = fail(IXH_EHIP, "modernbert: hip: event record failed");
+      return -1;
+    }
+    return used++;
+  }
+  void end(int idx, const char *name, double ops, double bytes) {
+    if (idx < 0) return;
+    if (hipEventRecord(w->events[2 * idx + 1], st) != hipSuccess) {
+      err = fail(IXH_EHIP, "modernbert: hip: event record failed");
+      return;
+    }
+    recs.push_back({name, idx, ops, bytes});
+  }
+  int flush() {
+    if (!on || err) return err;
+    std::lock_guard<std::mutex> lk(m->prof_mu);
+    for (const Rec &r : recs) {
+      float ms = 0.f;
+      HIPCK(hipEventElapsedTime(&ms, w->events[2 * r.idx], w->events[2 * r.idx + 1]));
+      StatAcc *s = nullptr;
+      for (auto &x : m->stats)
+        if (x.name == r.name) s = &x;
+      if (!s) {
+        m->stats.push_back(StatAcc{r.name});
+        s = &m->stats.back();
+      }
+      s->launches++;
+      s->ms += ms;
+      s->ops += r.ops;
+      s->bytes += r.bytes;
+    }
+    return IXH_OK;
+  }
+};
+
 // The forward pass. ids/out are device pointers here.
 int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
             const int32_t *offs, int B, int out_kind, float *d_out) {
@@ -402,8 +476,29 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   if ((rc = rope_for(m, 1, T, &rc_g, &rs_g, hold)) || (rc = rope_for(m, 0, T, &rc_l, &rs_l, hold)))
     return rc;
 
-  launch_positions(w->offs.as<int32_t>(), w->padoff.as<int32_t>(), B, w->pos.as<int32_t>(), nullptr, st);
-  LAUNCHCK("positions");
+  Prof prof{m, w, st, m->profiling.load()};
+#define RUN(name, ops, bytes, stmt)                                                      \
+  do {                                                                                   \
+    const int pi_ = prof.begin();                                                        \
+    stmt;                                                                                \
+    LAUNCHCK(name);                                                                      \
+    prof.end(pi_, name, (double)(ops), (double)(bytes));                                 \
+  } while (0)
+
+  // algorithmic figures: valid (query, key) pairs of local and global layers
+  double keys_local = 0, keys_global = 0;
+  const int Wl = c.local_attention / 2;
+  for (int b = 0; b < B; b++) {
+    const double n = offs[b + 1] - offs[b];
+    keys_global += n * n;
+    for (int i = 0; i < (int)n; i++)
+      keys_local += std::min((int)n, i + Wl + 1) - std::max(0, i - Wl);
+  }
+  const double dN = N, dH = H, dI = I;
+  const double row_bytes = m->emb_format == 0 ? 4 * dH : m->emb_format == 1 ? 2 * dH : dH + 4;
+
+  RUN("positions", 0, 8.0 * N,
+      launch_positions(w->offs.as<int32_t>(), w->padoff.as<int32_t>(), B, w->pos.as<int32_t>(), nullptr, st));
 
   // embedding gather + embeddings.norm (infer.go:361-368) -> x; layer 0's
   // QKV reads x itself (no attn_norm, infer.go:384-389): quantise it here.
@@ -425,8 +520,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   ra.q = w->xq.as<int8_t>();
   ra.ldq = KpH;
   ra.sa = w->sa.as<float>();
-  launch_rownorm(ra, st);
-  LAUNCHCK("embeddings");
+  RUN("emb_ln_quant", 0, dN * (4 + row_bytes + 4 * dH + dH + 4), launch_rownorm(ra, st));
 
   auto gemm = [&](int epi, const Mat &M, int Kp, float *C, int ldc, int n_valid) {
     GemmArgs g{};
@@ -447,6 +541,11 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     g.lanes = c.lanes;
     g.n_gelu = gelu_fma_cols(I, c.lanes);
     return g;
+  };
+  // GEMM HBM bytes: activations int8 + scales, weights, output (read too
+  // when accumulated)
+  auto gemm_bytes = [&](double k, double n, double out_cols, bool acc) {
+    return dN * (k + 4) + k * n + 12 * n + dN * out_cols * 4 * (acc ? 2 : 1);
   };
 
   AttnArgs aa{};
@@ -470,22 +569,23 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   aa.nblocks = nblocks;
   aa.ctx = w->ctx.as<float>();
 
+  RowArgs ln{};
+  ln.M = N;
+  ln.H = H;
+  ln.x = w->x.as<float>();
+  ln.eps = c.norm_eps;
+  ln.lanes = c.lanes;
+  ln.q = w->xq.as<int8_t>();
+  ln.ldq = KpH;
+  ln.sa = w->sa.as<float>();
+  const double ln_bytes = dN * (4 * dH + dH + 4);
+
   for (int l = 0; l < c.layers; l++) {
     const auto &L = m->layers[l];
     const bool global = l % c.global_every == 0;  // Config.IsGlobal
     if (l > 0) {
-      RowArgs r{};
-      r.M = N;
-      r.H = H;
-      r.x = w->x.as<float>();
-      r.gamma = L.attn_norm.as<float>();
-      r.eps = c.norm_eps;
-      r.lanes = c.lanes;
-      r.q = w->xq.as<int8_t>();
-      r.ldq = KpH;
-      r.sa = w->sa.as<float>();
-      launch_rownorm(r, st);
-      LAUNCHCK("attn_norm");
+      ln.gamma = L.attn_norm.as<float>();
+      RUN("ln_quant", 0, ln_bytes, launch_rownorm(ln, st));
     }
     // QKV projection with RoPE on the queries and keys (infer.go:390-399)
     GemmArgs g = gemm(EPI_ROPE, L.qkv, KpH, w->qkv.as<float>(), 3 * H, 3 * H);
@@ -493,43 +593,31 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     g.rope_sin = global ? rs_g : rs_l;
     g.pos = w->pos.as<int32_t>();
     g.rope_cols = 2 * H;
-    launch_gemm(EPI_ROPE, g, st);
-    LAUNCHCK("qkv");
+    RUN("gemm_qkv", 2 * dN * 3 * dH * dH, gemm_bytes(dH, 3 * dH, 3 * dH, false) + 4 * dN,
+        launch_gemm(EPI_ROPE, g, st));
     // attention (infer.go:437-518)
     aa.window = global ? -1 : c.local_attention / 2;
-    launch_attn_prologue(aa, st);
-    LAUNCHCK("attn_prologue");
-    launch_attn_main(aa, st);
-    LAUNCHCK("attn_main");
+    RUN("attn_prologue", 0, dN * 3 * dH * 4 + dN * 3 * dH + 8 * dN * nh,
+        launch_attn_prologue(aa, st));
+    const double pairs = global ? keys_global : keys_local;
+    RUN(global ? "attn_global" : "attn_local", 4.0 * D * nh * pairs,
+        dN * 3 * dH + 8 * dN * nh + dN * dH * 4, launch_attn_main(aa, st));
     // x += ctx . Wo^T (infer.go:403)
-    launch_quant_rows(w->ctx.as<float>(), H, N, H, w->xq.as<int8_t>(), KpH, w->sa.as<float>(), st);
-    LAUNCHCK("quant_ctx");
+    RUN("quant_ctx", 0, dN * (4 * dH + dH + 4),
+        launch_quant_rows(w->ctx.as<float>(), H, N, H, w->xq.as<int8_t>(), KpH, w->sa.as<float>(), st));
     g = gemm(EPI_ACCUM, L.o, KpH, w->x.as<float>(), H, H);
-    launch_gemm(EPI_ACCUM, g, st);
-    LAUNCHCK("wo");
+    RUN("gemm_wo", 2 * dN * dH * dH, gemm_bytes(dH, dH, dH, true), launch_gemm(EPI_ACCUM, g, st));
     // mlp_norm, Wi + GeGLU, x += g . WoMLP^T (infer.go:404-424)
-    {
-      RowArgs r{};
-      r.M = N;
-      r.H = H;
-      r.x = w->x.as<float>();
-      r.gamma = L.mlp_norm.as<float>();
-      r.eps = c.norm_eps;
-      r.lanes = c.lanes;
-      r.q = w->xq.as<int8_t>();
-      r.ldq = KpH;
-      r.sa = w->sa.as<float>();
-      launch_rownorm(r, st);
-      LAUNCHCK("mlp_norm");
-    }
+    ln.gamma = L.mlp_norm.as<float>();
+    RUN("ln_quant", 0, ln_bytes, launch_rownorm(ln, st));
     g = gemm(EPI_GEGLU, L.i, KpH, w->g.as<float>(), I, I);
-    launch_gemm(EPI_GEGLU, g, st);
-    LAUNCHCK("wi");
-    launch_quant_rows(w->g.as<float>(), I, N, I, w->xq.as<int8_t>(), KpI, w->sa.as<float>(), st);
-    LAUNCHCK("quant_g");
-    g = gemm(EPI_ACCUM, L.omlp, KpI, w->x.as<float>(), H, H);
-    launch_gemm(EPI_ACCUM, g, st);
-    LAUNCHCK("womlp");
+    RUN("gemm_wi", 2 * dN * 2 * dI * dH, gemm_bytes(dH, 2 * dI, dI, false),
+        launch_gemm(EPI_GEGLU, g, st));
+    RUN("quant_g", 0, dN * (4 * dI + dI + 4),
+        launch_quant_rows(w->g.as<float>(), I, N, I, w->xq.as<int8_t>(), KpI, w->sa.as<float>(), st));
+    g = gemm(EPI_ACCUM_MLP, L.omlp, KpI, w->x.as<float>(), H, H);
+    RUN("gemm_womlp", 2 * dN * dH * dI, gemm_bytes(dI, dH, dH, true),
+        launch_gemm(EPI_ACCUM_MLP, g, st));
   }
   // final_norm (infer.go:427), then pooling or the token states
   {
@@ -541,16 +629,15 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     r.eps = c.norm_eps;
     r.lanes = c.lanes;
     r.out = out_kind == IXH_OUT_TOKENS ? d_out : w->xn.as<float>();
-    launch_rownorm(r, st);
-    LAUNCHCK("final_norm");
+    RUN("final_norm", 0, dN * 8 * dH, launch_rownorm(r, st));
   }
-  if (out_kind == IXH_OUT_POOLED) {
-    launch_pool(w->xn.as<float>(), w->offs.as<int32_t>(), B, H, c.pooling == IXH_POOL_CLS, d_out, st);
-    LAUNCHCK("pool");
-  }
+  if (out_kind == IXH_OUT_POOLED)
+    RUN("pool", 0, dN * 4 * dH + (double)B * 4 * dH,
+        launch_pool(w->xn.as<float>(), w->offs.as<int32_t>(), B, H, c.pooling == IXH_POOL_CLS, d_out, st));
+#undef RUN
   // tables used by queued work stay alive until the stream has run them
   HIPCK(hipStreamSynchronize(st));
-  return IXH_OK;
+  return prof.flush();
 }
 
 int check_offs(const int32_t *offs, int B) {
@@ -750,6 +837,30 @@ int ixh_model_invalidate(ixh_model *m) {
   DEVGUARD(m->device);
   for (auto &L : m->layers) {
     L.qkv.set = L.o.set = L.i.set = L.omlp.set = false;
+  }
+  return IXH_OK;
+}
+
+int ixh_model_set_profiling(ixh_model *m, int on) {
+  if (!m) return fail(IXH_EINVAL, "modernbert: nil model");
+  std::lock_guard<std::mutex> lk(m->prof_mu);
+  m->stats.clear();
+  m->profiling.store(on != 0);
+  return IXH_OK;
+}
+
+int ixh_model_profile(ixh_model *m, ixh_kernel_stat *out, int cap, int *n) {
+  if (!m || !n || cap < 0 || (cap > 0 && !out)) return fail(IXH_EINVAL, "modernbert: bad arguments");
+  std::lock_guard<std::mutex> lk(m->prof_mu);
+  *n = (int)m->stats.size();
+  for (int i = 0; i < cap && i < (int)m->stats.size(); i++) {
+    const StatAcc &s = m->stats[i];
+    memset(&out[i], 0, sizeof out[i]);
+    snprintf(out[i].name, sizeof out[i].name, "%s", s.name.c_str());
+    out[i].launches = s.launches;
+    out[i].ms = s.ms;
+    out[i].ops = s.ops;
+    out[i].bytes = s.bytes;
   }
   return IXH_OK;
 }

@@ -16,6 +16,7 @@ enum GemmEpi {
   EPI_TILE = 2,    // Ci[m][n] = reference int32 tile (tests)
   EPI_GEGLU = 3,   // G[m][j] = gelu(deq a)*deq b, B rows interleaved by 32
   EPI_ROPE = 4,    // C[m][n] = deq, RoPE on columns < rope_cols
+  EPI_ACCUM_MLP = 5,  // EPI_ACCUM as a kernel of its own (WoMLP), for profiles
 };
 
 struct GemmArgs {

@@ -269,6 +269,20 @@ class Model:
                                              kind, C.c_void_p(out_ptr),
                                              C.c_void_p(stream) if stream else None))
 
+    def set_profiling(self, on):
+        """Per-kernel HIP-event timing of every encode (clears the sums)."""
+        _lib.check(self._L.ixh_model_set_profiling(self._h, 1 if on else 0))
+
+    def profile(self):
+        """{kernel class: dict(launches, ms, ops, bytes)} summed since
+        profiling was turned on."""
+        n = C.c_int(0)
+        _lib.check(self._L.ixh_model_profile(self._h, None, 0, C.byref(n)))
+        arr = (_lib.IxhKernelStat * max(n.value, 1))()
+        _lib.check(self._L.ixh_model_profile(self._h, arr, n.value, C.byref(n)))
+        return {a.name.decode(): dict(launches=a.launches, ms=a.ms, ops=a.ops, bytes=a.bytes)
+                for a in arr[:n.value]}
+
     def head_logits(self, x, w, b):
         """head.logits (heads.go:63-74) of rows x: [T, rows] float64."""
         x = np.ascontiguousarray(x, np.float32)
