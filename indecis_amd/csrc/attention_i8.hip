@@ -44,43 +44,54 @@ __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
   return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | (d << 24);
 }
 
+// K mean and V max per (sequence, head), then K and V quantised. Q was
+// quantised by the QKV GEMM epilogue. 16 threads own a row (a float4 of
+// the head's 64 values each); K goes through LDS 64 keys at a time so the
+// 64 sequential float32 chains of the mean read it from LDS.
 __global__ __launch_bounds__(256) void attn_prologue_kernel(AttnArgs a) {
-  __shared__ float mean[D];
-  __shared__ float vmaxp[3][D];
-  __shared__ float vinv[D];
+  __shared__ __attribute__((aligned(16))) float kst[64 * D];
+  __shared__ float vmaxp[16][D];
+  __shared__ float mean[D], vinv[D];
+  __shared__ __attribute__((aligned(16))) int8_t vtile[D][64 + 16];
   const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int sub = tid & 15, rg = tid >> 4;
   const int base = a.offs[b], n = a.offs[b + 1] - base;
   const int slot0 = a.padoff[b];
   const int npad = (n + kKeyPad - 1) / kKeyPad * kKeyPad;
   const int H = a.H, ld = 3 * H;
-  const float *qcol = a.qkv + (size_t)base * ld + h * D;
-  const float *kcol = qcol + H;
-  const float *vcol = qcol + 2 * H;
+  const float *kcol = a.qkv + (size_t)base * ld + H + h * D + 4 * sub;
+  const float *vcol = kcol + H;
 
-  if (tid < D) {
-    // mean[d]: AddTo over the keys in order, then Scale by 1/n
-    // (attention8.go:224-229).
-    float m = 0.f;
-    int j = 0;
-    for (; j + 8 <= n; j += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = kcol[(size_t)(j + u) * ld + tid];
-#pragma unroll
-      for (int u = 0; u < 8; u++) m = m + v[u];
+  // pass 1: sum of K in key order (AddTo, attention8.go:224-228) and
+  // max |V| per dimension (MaxAbsTo, attention8.go:259-261)
+  float ksum = 0.f;
+  float4 vm = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int c0 = 0; c0 < n; c0 += 64) {
+    for (int rr = rg; rr < 64; rr += 16) {
+      const int j = c0 + rr;
+      if (j < n) {
+        *(float4 *)&kst[rr * D + 4 * sub] = *(const float4 *)(kcol + (size_t)j * ld);
+        const float4 v = *(const float4 *)(vcol + (size_t)j * ld);
+        vm = make_float4(fmax32(vm.x, fabsf(v.x)), fmax32(vm.y, fabsf(v.y)),
+                         fmax32(vm.z, fabsf(v.z)), fmax32(vm.w, fabsf(v.w)));
+      }
     }
-    for (; j < n; j++) m = m + kcol[(size_t)j * ld + tid];
-    mean[tid] = n > 0 ? m * (1.0f / (float)n) : 0.f;
-  } else {
-    // per-dimension max |v| (MaxAbsTo, attention8.go:259-261), 3 partials
-    const int g = (tid >> 6) - 1, d = tid & 63;
-    float m = 0.f;
-    for (int j = g; j < n; j += 3) m = fmax32(m, fabsf(vcol[(size_t)j * ld + d]));
-    vmaxp[g][d] = m;
+    __syncthreads();
+    if (tid < D) {
+      const int cnt = min(64, n - c0);
+      for (int rr = 0; rr < cnt; rr++) ksum = ksum + kst[rr * D + tid];
+    }
+    __syncthreads();
   }
+  vmaxp[rg][4 * sub] = vm.x;
+  vmaxp[rg][4 * sub + 1] = vm.y;
+  vmaxp[rg][4 * sub + 2] = vm.z;
+  vmaxp[rg][4 * sub + 3] = vm.w;
   __syncthreads();
   if (tid < D) {
-    float vs = fmax32(fmax32(vmaxp[0][tid], vmaxp[1][tid]), vmaxp[2][tid]);
+    mean[tid] = n > 0 ? ksum * (1.0f / (float)n) : 0.f;  // Scale(mean, 1/n)
+    float vs = 0.f;
+    for (int g = 0; g < 16; g++) vs = fmax32(vs, vmaxp[g][tid]);
     float vi = 0.f;
     if (vs > 0.f) {  // attention8.go:262-269
       vs = vs / 127.0f;
@@ -91,78 +102,69 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(AttnArgs a) {
   }
   __syncthreads();
 
+  // pass 2: K centred and quantised per key (quantRowAVX2 without the
+  // flip, attention8.go:240-251), V per dimension (quantCols,
+  // attention8.go:270-279) and transposed through LDS
   int8_t *kp = a.kp + ((size_t)h * a.Npad + slot0) * D;
   float *ks = a.ks + (size_t)h * a.Npad + slot0;
   int8_t *vt = a.vt + (size_t)h * D * a.Npad + slot0;
-  for (int j = tid; j < npad; j += 256) {
-    if (j >= n) {  // zero slots up to the 64-key boundary
-      v4i z = {0, 0, 0, 0};
-#pragma unroll
-      for (int c = 0; c < 4; c++) *(v4i *)(kp + (size_t)j * D + 16 * c) = z;
-      ks[j] = 0.f;
-      for (int d = 0; d < D; d++) vt[(size_t)d * a.Npad + j] = 0;
-      continue;
-    }
-    float4 v[16];
-    // Q: per row, scale*score scale (attention8.go:211-220)
-    const float *qr = qcol + (size_t)j * ld;
-#pragma unroll
-    for (int c = 0; c < 16; c++) v[c] = *(const float4 *)(qr + 4 * c);
-    float mx = absmax16(v);
-    float s = 0.f, inv = 0.f;
-    if (mx != 0.f) {
-      s = mx / 127.0f;
-      inv = 1.0f / s;
-    }
-    int8_t *qdst = a.qq + (size_t)(base + j) * H + h * D;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      v4i w;
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const float4 f = v[4 * c + u];
-        w[u] = pack4(q8(f.x, inv), q8(f.y, inv), q8(f.z, inv), q8(f.w, inv));
+  const float4 mu = *(const float4 *)&mean[4 * sub];
+  const float4 vi = *(const float4 *)&vinv[4 * sub];
+  for (int c0 = 0; c0 < npad; c0 += 64) {
+    for (int rr = rg; rr < 64; rr += 16) {
+      const int j = c0 + rr;
+      int kq = 0, v0 = 0, v1 = 0, v2 = 0, v3 = 0;
+      float s = 0.f;
+      if (j < n) {
+        const float4 k = *(const float4 *)(kcol + (size_t)j * ld);
+        const float4 c = make_float4(k.x - mu.x, k.y - mu.y, k.z - mu.z, k.w - mu.w);
+        float mx = fmax32(fmax32(fabsf(c.x), fabsf(c.y)), fmax32(fabsf(c.z), fabsf(c.w)));
+        for (int t = 1; t < 16; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t, 16));
+        float inv = 0.f;
+        if (mx != 0.f) {
+          s = mx / 127.0f;
+          inv = 1.0f / s;
+        }
+        kq = pack4(q8(c.x, inv), q8(c.y, inv), q8(c.z, inv), q8(c.w, inv));
+        const float4 v = *(const float4 *)(vcol + (size_t)j * ld);
+        v0 = q8(v.x, vi.x);
+        v1 = q8(v.y, vi.y);
+        v2 = q8(v.z, vi.z);
+        v3 = q8(v.w, vi.w);
       }
-      *(v4i *)(qdst + 16 * c) = w;
+      *(int *)(kp + (size_t)j * D + 4 * sub) = kq;
+      if (sub == 0) ks[j] = s;
+      vtile[4 * sub][rr] = (int8_t)v0;
+      vtile[4 * sub + 1][rr] = (int8_t)v1;
+      vtile[4 * sub + 2][rr] = (int8_t)v2;
+      vtile[4 * sub + 3][rr] = (int8_t)v3;
     }
-    a.sq[(size_t)(base + j) * a.nh + h] = s * a.scale;
-    // K: centred, per key (attention8.go:240-251)
-    const float *kr = kcol + (size_t)j * ld;
-#pragma unroll
-    for (int c = 0; c < 16; c++) {
-      const float4 f = *(const float4 *)(kr + 4 * c);
-      v[c] = make_float4(f.x - mean[4 * c], f.y - mean[4 * c + 1], f.z - mean[4 * c + 2],
-                         f.w - mean[4 * c + 3]);
+    __syncthreads();
+    {
+      const int d = tid >> 2, seg = tid & 3;
+      *(v4i *)(vt + (size_t)d * a.Npad + c0 + 16 * seg) = *(const v4i *)&vtile[d][16 * seg];
     }
-    mx = absmax16(v);
-    s = 0.f;
-    inv = 0.f;
-    if (mx != 0.f) {
-      s = mx / 127.0f;
-      inv = 1.0f / s;
-    }
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      v4i w;
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const float4 f = v[4 * c + u];
-        w[u] = pack4(q8(f.x, inv), q8(f.y, inv), q8(f.z, inv), q8(f.w, inv));
-      }
-      *(v4i *)(kp + (size_t)j * D + 16 * c) = w;
-    }
-    ks[j] = s;
-    // V: per dimension (quantCols, attention8.go:270-279), transposed
-    const float *vr = vcol + (size_t)j * ld;
-#pragma unroll
-    for (int c = 0; c < 16; c++) {
-      const float4 f = *(const float4 *)(vr + 4 * c);
-      vt[(size_t)(4 * c) * a.Npad + j] = (int8_t)q8(f.x, vinv[4 * c]);
-      vt[(size_t)(4 * c + 1) * a.Npad + j] = (int8_t)q8(f.y, vinv[4 * c + 1]);
-      vt[(size_t)(4 * c + 2) * a.Npad + j] = (int8_t)q8(f.z, vinv[4 * c + 2]);
-      vt[(size_t)(4 * c + 3) * a.Npad + j] = (int8_t)q8(f.w, vinv[4 * c + 3]);
-    }
+    __syncthreads();
   }
+}
+
+// Q per (row, head) for Attend8 callers whose queries did not come out of
+// the QKV GEMM epilogue: 16 threads per row, as the prologue's K pass.
+__global__ __launch_bounds__(256) void attn_quant_q_kernel(AttnArgs a) {
+  const int g = blockIdx.x * 16 + (threadIdx.x >> 4), sub = threadIdx.x & 15;
+  if (g >= a.N * a.nh) return;  // whole 16-lane groups leave together
+  const int row = g / a.nh, h = g % a.nh;
+  const float4 v = *(const float4 *)(a.qkv + (size_t)row * 3 * a.H + h * D + 4 * sub);
+  float mx = fmax32(fmax32(fabsf(v.x), fabsf(v.y)), fmax32(fabsf(v.z), fabsf(v.w)));
+  for (int t = 1; t < 16; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t, 16));
+  float s = 0.f, inv = 0.f;
+  if (mx != 0.f) {
+    s = mx / 127.0f;
+    inv = 1.0f / s;
+  }
+  *(int *)(a.qq + (size_t)row * a.H + h * D + 4 * sub) =
+      pack4(q8(v.x, inv), q8(v.y, inv), q8(v.z, inv), q8(v.w, inv));
+  if (sub == 0) a.sq[(size_t)row * a.nh + h] = s * a.scale;
 }
 
 template <bool GLOBAL>
@@ -346,6 +348,12 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
 }
 
 }  // namespace
+
+void launch_attn_quant_q(const AttnArgs &a, hipStream_t s) {
+  const long groups = (long)a.N * a.nh;
+  if (groups <= 0) return;
+  attn_quant_q_kernel<<<(unsigned)((groups + 15) / 16), 256, 0, s>>>(a);
+}
 
 void launch_attn_prologue(const AttnArgs &a, hipStream_t s) {
   if (a.B <= 0) return;

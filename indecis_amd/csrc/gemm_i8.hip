@@ -142,6 +142,24 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
           v0 = x1 * c - x2 * s;
           v1 = x2 * c + x1 * s;
         }
+        if (nw < a.q_cols) {
+          // the query head, quantised per row as Attn8.Prepare does
+          // (attention8.go:211-220): the 64 values of the row are this
+          // lane's two and those of the 31 other lanes of its half-wave.
+          float mx = fmax32(fabsf(v0), fabsf(v1));
+#pragma unroll
+          for (int t = 1; t < 32; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t));
+          float sc = 0.f, inv = 0.f;
+          if (mx != 0.f) {
+            sc = mx / 127.0f;
+            inv = 1.0f / sc;
+          }
+          int8_t *qrow = a.qq + (size_t)m * a.q_cols + nw;
+          qrow[fr] = (int8_t)q8(v0, inv);
+          qrow[32 + fr] = (int8_t)q8(v1, inv);
+          if (fr == 0) a.sq[(size_t)m * (a.q_cols / 64) + nw / 64] = sc * a.attn_scale;
+          continue;
+        }
         float *row = a.C + (size_t)m * a.ldc;
         if (ncol[0] < a.n_valid) row[ncol[0]] = v0;
         if (ncol[1] < a.n_valid) row[ncol[1]] = v1;

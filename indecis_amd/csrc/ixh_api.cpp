@@ -593,11 +593,15 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     g.rope_sin = global ? rs_g : rs_l;
     g.pos = w->pos.as<int32_t>();
     g.rope_cols = 2 * H;
-    RUN("gemm_qkv", 2 * dN * 3 * dH * dH, gemm_bytes(dH, 3 * dH, 3 * dH, false) + 4 * dN,
-        launch_gemm(EPI_ROPE, g, st));
+    g.q_cols = H;  // queries quantised per head in the epilogue
+    g.qq = w->qq.as<int8_t>();
+    g.sq = w->sq.as<float>();
+    g.attn_scale = aa.scale;
+    RUN("gemm_qkv", 2 * dN * 3 * dH * dH,
+        gemm_bytes(dH, 3 * dH, 2 * dH, false) + dN * (4 + dH + 4 * nh), launch_gemm(EPI_ROPE, g, st));
     // attention (infer.go:437-518)
     aa.window = global ? -1 : c.local_attention / 2;
-    RUN("attn_prologue", 0, dN * 3 * dH * 4 + dN * 3 * dH + 8 * dN * nh,
+    RUN("attn_prologue", 0, dN * 2 * dH * 4 + dN * 2 * dH + 4 * dN * nh,
         launch_attn_prologue(aa, st));
     const double pairs = global ? keys_global : keys_local;
     RUN(global ? "attn_global" : "attn_local", 4.0 * D * nh * pairs,
@@ -1241,6 +1245,8 @@ int ixh_attend8(int device, float *o, const float *q, const float *k, const floa
   aa.blocks = dblocks.as<int32_t>();
   aa.nblocks = (int)blocks.size() / 2;
   aa.ctx = dctx.as<float>();
+  launch_attn_quant_q(aa, ts.s);
+  LAUNCHCK("attn_quant_q");
   launch_attn_prologue(aa, ts.s);
   LAUNCHCK("attn_prologue");
   launch_attn_main(aa, ts.s);

@@ -39,6 +39,13 @@ struct GemmArgs {
   int rope_cols;                     // columns < rope_cols are rotated (2H)
   int lanes;                         // Go simd width, for the GeGLU tail rule
   int n_gelu;                        // GEGLU: I (gated width), for the tail rule
+  // EPI_ROPE: columns < q_cols are the queries, quantised per (row, head)
+  // into qq [M][q_cols] and sq [M][q_cols/64] (times attn_scale) instead
+  // of being stored in C
+  int q_cols;
+  int8_t *qq;
+  float *sq;
+  float attn_scale;
 };
 
 void launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
@@ -104,6 +111,7 @@ struct AttnArgs {
   int nblocks;
   float *ctx;              // [N][H]
 };
+void launch_attn_quant_q(const AttnArgs &a, hipStream_t s);
 void launch_attn_prologue(const AttnArgs &a, hipStream_t s);
 void launch_attn_main(const AttnArgs &a, hipStream_t s);
 

@@ -11,6 +11,8 @@
 #include "ixh_device.h"
 #include "ixh_internal.h"
 
+#include <algorithm>
+
 namespace ixh {
 
 namespace {
@@ -61,6 +63,50 @@ struct RowSrc {
     if (f32) return f32[i];
     if (bf16) return __uint_as_float((unsigned)bf16[i] << 16);
     return (float)i8[i] * i8s;
+  }
+};
+
+// Branch-free row source for the LDS kernel: SRC 0 f32 rows of a.x, 1 the
+// f32 table, 2 the bf16 table (+ exact f32 rows), 3 the int8 table. The
+// row is wave-uniform, so the only branch (bf16 vs exact) is scalar.
+template <int SRC>
+struct RowLoad {
+  const float *f = nullptr;
+  const uint16_t *h = nullptr;
+  const int8_t *b = nullptr;
+  float s = 0.f;
+  __device__ RowLoad(const RowArgs &a, int R) {
+    if constexpr (SRC == 0) {
+      f = a.x + (size_t)R * a.H;
+    } else {
+      const int id = a.ids[R];
+      if constexpr (SRC == 1) {
+        f = a.emb_f32 + (size_t)id * a.H;
+      } else if constexpr (SRC == 2) {
+        const int slot = a.exact_slot[id];
+        if (slot >= 0)
+          f = a.exact_rows + (size_t)slot * a.H;
+        else
+          h = a.emb_bf16 + (size_t)id * a.H;
+      } else {
+        b = a.emb_i8 + (size_t)id * a.H;
+        s = a.emb_i8_scale[id];
+      }
+    }
+  }
+  __device__ float4 load4(int i) const {
+    if constexpr (SRC == 3) {
+      const int w = *(const int *)(b + i);
+      return make_float4((float)(int8_t)(w & 0xff) * s, (float)(int8_t)((w >> 8) & 0xff) * s,
+                         (float)(int8_t)((w >> 16) & 0xff) * s, (float)(int8_t)(w >> 24) * s);
+    } else if constexpr (SRC == 2) {
+      if (f) return *(const float4 *)(f + i);
+      const uint2 u = *(const uint2 *)(h + i);
+      return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                         __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+    } else {
+      return *(const float4 *)(f + i);
+    }
   }
 };
 
@@ -174,6 +220,103 @@ __global__ __launch_bounds__(256) void rownorm_kernel(RowArgs a) {
   }
 }
 
+// LayerNorm (+ quantisation) for lanes V in {4, 8, 16} and H = 256*CPL:
+// one wave owns RPW = 64/V rows. Lane t holds columns 4*(t + 64c) of each
+// row in registers (coalesced float4 loads, every load of the wave in
+// flight before the first wait) and copies them to LDS; lane (r, l) =
+// (t / V, t % V) then runs the reference's lane partial l of row r —
+// x[l], x[l+V], ... added in order — from LDS, so all 64 lanes carry one of
+// the sequential chains. The output and quantisation passes use the
+// registers. Rows are padded by V floats in LDS (conflict-free chains).
+template <int V, int CPL, int SRC>
+__global__ __launch_bounds__(64) void rownorm_lds_kernel(RowArgs a) {
+  constexpr int RPW = 64 / V, H = 256 * CPL, LD = H + V;
+  __shared__ __attribute__((aligned(16))) float xs[RPW * LD];
+  __shared__ float rmean[RPW], rrstd[RPW];
+  const int lane = threadIdx.x;
+  const int row0 = blockIdx.x * RPW;
+  float4 x[RPW][CPL];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int R = min(row0 + r, a.M - 1);  // rows past M repeat the last one
+    const RowLoad<SRC> src(a, R);
+#pragma unroll
+    for (int c = 0; c < CPL; c++) x[r][c] = src.load4(4 * (lane + 64 * c));
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int c = 0; c < CPL; c++) *(float4 *)&xs[r * LD + 4 * (lane + 64 * c)] = x[r][c];
+  const bool ln = a.gamma != nullptr;
+  if (ln) {
+    __syncthreads();
+    const int r = lane / V, l = lane % V;
+    const float *xr = &xs[r * LD + l];
+    float p = 0.f;
+#pragma unroll
+    for (int k = 0; k < H / V; k++) p = p + xr[V * k];
+    double sum = 0.0;  // lanes in order, in float64 (vec_simd.go:294-297)
+#pragma unroll
+    for (int t = 0; t < V; t++) sum += (double)__shfl(p, r * V + t);
+    const float mean = (float)(sum / (double)H);
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < H / V; k++) {
+      const float d = xr[V * k] - mean;
+      q = __builtin_fmaf(d, d, q);
+    }
+    double var = 0.0;
+#pragma unroll
+    for (int t = 0; t < V; t++) var += (double)__shfl(q, r * V + t);
+    if (l == 0) {
+      rmean[r] = mean;
+      rrstd[r] = (float)(1.0 / __builtin_sqrt(var / (double)H + a.eps));
+    }
+    __syncthreads();
+  }
+  float4 g[CPL];
+  if (ln) {
+#pragma unroll
+    for (int c = 0; c < CPL; c++) g[c] = *(const float4 *)&a.gamma[4 * (lane + 64 * c)];
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int R = row0 + r;
+    if (R >= a.M) break;  // wave-uniform
+    float mx = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+      float4 v = x[r][c];
+      if (ln) {
+        const float mean = rmean[r], rstd = rrstd[r];
+        v = make_float4(((v.x - mean) * rstd) * g[c].x, ((v.y - mean) * rstd) * g[c].y,
+                        ((v.z - mean) * rstd) * g[c].z, ((v.w - mean) * rstd) * g[c].w);
+        x[r][c] = v;
+      }
+      if (a.out) *(float4 *)(a.out + (size_t)R * H + 4 * (lane + 64 * c)) = v;
+      mx = fmax32(mx, fmax32(fmax32(fabsf(v.x), fabsf(v.y)), fmax32(fabsf(v.z), fabsf(v.w))));
+    }
+    if (!a.q) continue;
+#pragma unroll
+    for (int t = 1; t < 64; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t));
+    float s = 0.f, inv = 0.f;
+    if (mx != 0.f) {  // quantizeA (linalg/int8.go:160-191)
+      s = mx / 127.0f;
+      inv = 1.0f / s;
+    }
+    int8_t *qrow = a.q + (size_t)R * a.ldq;
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+      const float4 v = x[r][c];
+      const int q0 = q8(v.x, inv), q1 = q8(v.y, inv), q2 = q8(v.z, inv), q3 = q8(v.w, inv);
+      *(int *)(qrow + 4 * (lane + 64 * c)) =
+          (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+    }
+    for (int i = H + lane; i < a.ldq; i += 64) qrow[i] = 0;
+    if (lane == 0) a.sa[R] = s;
+  }
+}
+
 // One wave per row: quantizeA on rows of f32 (no LayerNorm).
 __global__ __launch_bounds__(256) void quant_rows_kernel(const float *x, int ld, int M, int K,
                                                          int8_t *q, int ldq, float *sa) {
@@ -249,6 +392,24 @@ __global__ void head_logits_kernel(const float *x, int T, int H, const float *w,
 
 void launch_rownorm(const RowArgs &a, hipStream_t s) {
   if (a.M <= 0) return;
+  const int src = !a.ids ? 0 : a.emb_format == 0 ? 1 : a.emb_format == 1 ? 2 : 3;
+  if (a.lanes > 0 && a.H % 256 == 0 && a.H <= 1024 && !(a.lanes == 4 && a.H > 768)) {
+    const int V = a.lanes, cpl = a.H / 256, rpw = 64 / V;
+    const dim3 grid((a.M + rpw - 1) / rpw);
+#define IXH_LN(VV, CC)                                                                   \
+  if (V == VV && cpl == CC) {                                                            \
+    switch (src) {                                                                       \
+    case 0: rownorm_lds_kernel<VV, CC, 0><<<grid, 64, 0, s>>>(a); return;               \
+    case 1: rownorm_lds_kernel<VV, CC, 1><<<grid, 64, 0, s>>>(a); return;               \
+    case 2: rownorm_lds_kernel<VV, CC, 2><<<grid, 64, 0, s>>>(a); return;               \
+    default: rownorm_lds_kernel<VV, CC, 3><<<grid, 64, 0, s>>>(a); return;              \
+    }                                                                                    \
+  }
+    IXH_LN(4, 1) IXH_LN(4, 2) IXH_LN(4, 3)
+    IXH_LN(8, 1) IXH_LN(8, 2) IXH_LN(8, 3) IXH_LN(8, 4)
+    IXH_LN(16, 1) IXH_LN(16, 2) IXH_LN(16, 3) IXH_LN(16, 4)
+#undef IXH_LN
+  }
   const int tpr = a.lanes <= 0 ? 1 : a.lanes / 4;
   const long threads = (long)a.M * tpr;
   dim3 grid((unsigned)((threads + 255) / 256)), block(256);
