@@ -200,6 +200,14 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
   const int ce = global ? n : min(n, qi + W + 1);
   const int V = a.lanes;
   const int ts = V > 0 ? cs + ((ce - cs) / V) * V : cs;
+  // wave-wide bounds over the active queries: a tile [k0, k0+32) with
+  // k0 >= cs_hi and k0+32 <= ts_lo is valid and exp-vector for every query
+  int cs_hi = qact ? cs : 0, ts_lo = qact ? ts : 1 << 30, ce_hi = qact ? ce : 0;
+  for (int t = 1; t < 64; t <<= 1) {
+    cs_hi = max(cs_hi, __shfl_xor(cs_hi, t));
+    ts_lo = min(ts_lo, __shfl_xor(ts_lo, t));
+    ce_hi = max(ce_hi, __shfl_xor(ce_hi, t));
+  }
 
   // key tiles (32 keys) of this wave and of the block
   int wt0, wt1, bk0, bk1;
@@ -215,6 +223,7 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
     bk1 = min(n, Q0 + kAttnQBlock - 1 + W + 1);
   }
   if (q0 >= n) wt1 = wt0;  // idle wave (still takes part in the barriers)
+  const bool one_chunk = bk1 - bk0 <= CHUNK;
 
   const int8_t *kglob = a.kp + ((size_t)h * a.Npad + slot0) * D;
   const float *ksglob = a.ks + (size_t)h * a.Npad + slot0;
@@ -250,14 +259,24 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
       *(v4i *)&Vs[d * VS + 32 * g + 16] = o1;
     }
   };
-  auto score_tile = [&](int t, int c0) -> v16i {
+  // Scores of tile t: ((f32(sum q*k)) * ks) * sq, in the S^T layout (rows
+  // = keys 8*(r/4) + 4*(lane/32) + r%4 of the tile, column = this query).
+  auto scores = [&](int t, int c0, float *sv) {
     v16i acc;
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0;
     const int8_t *kr = &Ks[(t * 32 - c0 + (lane & 31)) * KS + 16 * (lane >> 5)];
     acc = mfma32(*(const v4i *)kr, qb[0], acc);
     acc = mfma32(*(const v4i *)(kr + 32), qb[1], acc);
-    return acc;
+    const float *kt = &kss[t * 32 - c0 + 4 * (lane >> 5)];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const float4 k4 = *(const float4 *)(kt + 8 * g);
+      sv[4 * g] = ((float)acc[4 * g] * k4.x) * sqv;
+      sv[4 * g + 1] = ((float)acc[4 * g + 1] * k4.y) * sqv;
+      sv[4 * g + 2] = ((float)acc[4 * g + 2] * k4.z) * sqv;
+      sv[4 * g + 3] = ((float)acc[4 * g + 3] * k4.w) * sqv;
+    }
   };
 
   // ---- pass 1: row max of the valid scores ----
@@ -265,15 +284,22 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
   for (int c0 = bk0; c0 < bk1; c0 += CHUNK) {
     __syncthreads();
     stage_k(c0);
+    if (one_chunk) stage_v(c0);
     __syncthreads();
     const int t0 = max(wt0, c0 / 32), t1 = min(wt1, (c0 + CHUNK) / 32);
     for (int t = t0; t < t1; t++) {
-      const v16i acc = score_tile(t, c0);
+      float sv[16];
+      scores(t, c0, sv);
+      const int k0 = t * 32;
+      if (k0 >= cs_hi && k0 + 32 <= ts_lo) {  // every key valid for every query
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int j = t * 32 + acc_row(r, lane);
-        const float sv = ((float)acc[r] * kss[j - c0]) * sqv;
-        if (j >= cs && j < ce) m = fmax32(m, sv);
+        for (int r = 0; r < 16; r++) m = fmax32(m, sv[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int j = k0 + acc_row(r, lane);
+          m = (j >= cs && j < ce) ? fmax32(m, sv[r]) : m;
+        }
       }
     }
   }
@@ -285,37 +311,46 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
   for (int dt = 0; dt < 2; dt++)
 #pragma unroll
     for (int r = 0; r < 16; r++) ohi[dt][r] = olo[dt][r] = 0;
-  int psum = 0;
+  unsigned psum = 0;
   for (int c0 = bk0; c0 < bk1; c0 += CHUNK) {
-    __syncthreads();
-    stage_k(c0);
-    stage_v(c0);
-    __syncthreads();
+    if (!one_chunk) {
+      __syncthreads();
+      stage_k(c0);
+      stage_v(c0);
+      __syncthreads();
+    }
     const int t0 = max(wt0, c0 / 32), t1 = min(wt1, (c0 + CHUNK) / 32);
     for (int t = t0; t < t1; t++) {
-      const v16i acc = score_tile(t, c0);
-      int hb[16], lb[16];
+      float sv[16];
+      scores(t, c0, sv);
+      const int k0 = t * 32;
+      const bool full = k0 >= cs_hi && k0 + 32 <= ts_lo;
+      const bool tail = k0 + 32 > ts_lo && k0 < ce_hi;  // some exp32 tail key here
+      unsigned pw[4];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int j = t * 32 + acc_row(r, lane);
-        const float sv = ((float)acc[r] * kss[j - c0]) * sqv;
-        int p = 0;
-        if (j >= cs && j < ce) {
-          const float v = sv - m;
+      for (int g = 0; g < 4; g++) {
+        unsigned w = 0;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int r = 4 * g + u;
+          const float v = sv[r] - m;
           float e = exp32_simd(v);
-          if (j >= ts) e = exp32_scalar(v);
-          p = (int)rne(e * 255.0f);  // QuantizeRowU8 (vec_simd.go:64-91)
+          if (!full) {
+            const int j = k0 + acc_row(r, lane);
+            if (tail) e = (j >= ts) ? exp32_scalar(v) : e;
+            e = (j >= cs && j < ce) ? e : 0.0f;
+          }
+          // QuantizeRowU8 (vec_simd.go:64-91): RNE(e*255) in [0, 255]
+          w = __builtin_amdgcn_cvt_pk_u8_f32(rne(e * 255.0f), u, w);
         }
-        psum += p;
-        hb[r] = p >> 7;
-        lb[r] = p & 127;
+        pw[g] = w;
+        psum = __builtin_amdgcn_udot4(w, 0x01010101u, psum, false);
       }
-      v4i bh, bl;
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        bh[u] = pack4(hb[4 * u], hb[4 * u + 1], hb[4 * u + 2], hb[4 * u + 3]);
-        bl[u] = pack4(lb[4 * u], lb[4 * u + 1], lb[4 * u + 2], lb[4 * u + 3]);
-      }
+      // P = 128*(P>>7) + (P&127): both halves fit int8
+      const v4i bh = {(int)((pw[0] >> 7) & 0x01010101u), (int)((pw[1] >> 7) & 0x01010101u),
+                      (int)((pw[2] >> 7) & 0x01010101u), (int)((pw[3] >> 7) & 0x01010101u)};
+      const v4i bl = {(int)(pw[0] & 0x7f7f7f7fu), (int)(pw[1] & 0x7f7f7f7fu),
+                      (int)(pw[2] & 0x7f7f7f7fu), (int)(pw[3] & 0x7f7f7f7fu)};
 #pragma unroll
       for (int dt = 0; dt < 2; dt++) {
         const v4i fv = *(const v4i *)&Vs[(dt * 32 + (lane & 31)) * VS + (t * 32 - c0) + 16 * (lane >> 5)];
@@ -326,22 +361,23 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
   }
   psum += __shfl_xor(psum, 32);
   if (!qact) return;
-  const float sp = 1.0f / (float)psum;
+  const float sp = 1.0f / (float)(int)psum;
   const float *vsd = a.vs + ((size_t)b * a.nh + h) * D;
   float *orow = a.ctx + (size_t)(base + qi) * H + h * D;
 #pragma unroll
   for (int dt = 0; dt < 2; dt++) {
 #pragma unroll
     for (int g = 0; g < 4; g++) {
+      const int d0 = dt * 32 + acc_row(4 * g, lane);
+      const float4 v4 = *(const float4 *)&vsd[d0];
+      const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
       float o[4];
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int r = 4 * g + u;
-        const int d = dt * 32 + acc_row(r, lane);
         const int tile = 128 * ohi[dt][r] + olo[dt][r];
-        o[u] = (((float)tile - 0.0f) * vsd[d]) * sp;
+        o[u] = (((float)tile - 0.0f) * vv[u]) * sp;
       }
-      const int d0 = dt * 32 + acc_row(4 * g, lane);
       *(float4 *)(orow + d0) = make_float4(o[0], o[1], o[2], o[3]);
     }
   }

@@ -9,10 +9,14 @@
 // rescales it with the same float32 operations in the same order:
 // ((f32(tile) - zc[n]) * sb[n]) * sa[m] (+ C).
 //
-// Block tile 128x128, K step 64, 256 threads (4 waves, 2x2), each wave a
-// 64x64 tile of 2x2 MFMA 32x32 blocks. A and B go global -> registers ->
-// LDS (double buffered, rows padded to 80 bytes so the 16-byte fragment
-// reads of 8 consecutive rows hit distinct banks).
+// Block tile 256x128, K step 64, 256 threads: 4 waves (2x2), each a 128x64
+// tile of 4x2 MFMA 32x32 blocks (128 accumulators). A and B stream into a
+// 3-stage LDS ring with direct-to-LDS loads (global_load_lds_dwordx4: a
+// wave instruction fills 1 KB, 16 rows of 64 bytes); the 16-byte chunks of
+// a row are XOR-swizzled by (row >> 1) & 3 so the 16-byte fragment reads of
+// consecutive rows fall in distinct banks. One barrier per K step; loads
+// run two K steps ahead. Tiles are handed out XCD by XCD so the N-tiles of
+// an A panel share one L2.
 #include "ixh_device.h"
 #include "ixh_internal.h"
 
@@ -20,82 +24,120 @@ namespace ixh {
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64, LS = 80;
+constexpr int BM = 256, BN = 128, BK = 64, STAGES = 3;
+constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK, STAGE_BYTES = A_BYTES + B_BYTES;
+constexpr int NXCD = 8;
+
+typedef __attribute__((address_space(3))) void *lds_ptr;
+typedef const __attribute__((address_space(1))) void *glb_ptr;
+
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 3; }
+
+// s_waitcnt with only the vector-memory count (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 template <int EPI>
-__global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) int8_t As[2][BM * LS];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN * LS];
+__global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int ntn = a.Np / BN;
-  const int nt = blockIdx.x % ntn, mt = blockIdx.x / ntn;
+  const int ntn = a.Np / BN, ntm = (a.M + BM - 1) / BM;
+  const int tiles = ntm * ntn;
+  // XCD-aware order: block b runs on XCD b % 8; give each XCD a contiguous
+  // run of tiles, N fastest.
+  const int per_xcd = (tiles + NXCD - 1) / NXCD;
+  const int tix = (blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
+  if (tix >= tiles) return;
+  const int nt = tix % ntn, mt = tix / ntn;
   const int m0 = mt * BM, n0 = nt * BN;
 
-  int lrow[2], lcol[2];
-  const int8_t *ag[2], *bg[2];
-  bool aok[2];
+  // This wave's direct-to-LDS loads of a stage: A chunks 4*wave..+3 (rows
+  // 64*wave + 16u + lane/4), B chunks 2*wave..+1 (rows 32*wave + 16u +
+  // lane/4). Lane i fills LDS bytes 16i of its chunk: row i/4, physical
+  // 16-byte column i%4, i.e. logical column (i%4) ^ swz(row).
+  const int lrow = lane >> 2, lchunk = (lane & 3) ^ swz(lane >> 2);
+  glb_ptr ag[4];
+  glb_ptr bg[2];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    int c = tid + 256 * i;
-    lrow[i] = c >> 2;
-    lcol[i] = (c & 3) * 16;
-    aok[i] = m0 + lrow[i] < a.M;
-    ag[i] = a.A + (size_t)(aok[i] ? m0 + lrow[i] : 0) * a.lda + lcol[i];
-    bg[i] = a.B + (size_t)(n0 + lrow[i]) * a.ldb + lcol[i];
+  for (int u = 0; u < 4; u++) {
+    int row = m0 + 64 * wave + 16 * u + lrow;
+    row = row < a.M ? row : a.M - 1;  // rows past M load row M-1 (never stored)
+    ag[u] = (glb_ptr)(a.A + (size_t)row * a.lda + 16 * lchunk);
   }
-  v4i ra[2], rb[2];
-  auto gload = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      v4i z = {0, 0, 0, 0};
-      ra[i] = aok[i] ? *(const v4i *)(ag[i] + k0) : z;
-      rb[i] = *(const v4i *)(bg[i] + k0);
-    }
-  };
-  auto lstore = [&](int buf) {
+  for (int u = 0; u < 2; u++)
+    bg[u] = (glb_ptr)(a.B + (size_t)(n0 + 32 * wave + 16 * u + lrow) * a.ldb + 16 * lchunk);
+
+  auto issue = [&](int kt) {
+    int8_t *st = smem + (kt % STAGES) * STAGE_BYTES;
+    const int k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      *(v4i *)&As[buf][lrow[i] * LS + lcol[i]] = ra[i];
-      *(v4i *)&Bs[buf][lrow[i] * LS + lcol[i]] = rb[i];
-    }
+    for (int u = 0; u < 4; u++)
+      __builtin_amdgcn_global_load_lds((glb_ptr)((const int8_t *)ag[u] + k0),
+                                       (lds_ptr)(st + (64 * wave + 16 * u) * BK), 16, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+      __builtin_amdgcn_global_load_lds((glb_ptr)((const int8_t *)bg[u] + k0),
+                                       (lds_ptr)(st + A_BYTES + (32 * wave + 16 * u) * BK), 16, 0, 0);
   };
 
-  v16i acc[2][2];
+  v16i acc[4][2];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
+  // per-row activation scales of the tile, for the epilogue
+  __shared__ float sa_s[BM];
+  sa_s[tid] = a.sa[min(m0 + tid, a.M - 1)];
+  __shared__ int pos_s[EPI == EPI_ROPE ? BM : 1];
+  if constexpr (EPI == EPI_ROPE) pos_s[tid] = a.pos[min(m0 + tid, a.M - 1)];
+
   const int nk = a.Kp / BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  const int fr = lane & 31, fk = (lane >> 5) * 16;
+  const int fr = lane & 31, fh = lane >> 5;
+  issue(0);
+  if (nk > 1) issue(1);
   for (int kt = 0; kt < nk; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * BK);
+    if (kt + 1 < nk)
+      wait_vmcnt<6>();  // this K step's 6 loads done, the next step's in flight
+    else
+      wait_vmcnt<0>();
+    // every wave's loads landed; stage (kt+2)%3 is free. A bare s_barrier:
+    // __syncthreads' fence would also drain the next stage's loads.
+    __builtin_amdgcn_s_barrier();
+    if (kt + 2 < nk) issue(kt + 2);
+    const int8_t *st = smem + (kt % STAGES) * STAGE_BYTES;
 #pragma unroll
     for (int s = 0; s < 2; s++) {
-      v4i fa[2], fb[2];
+      v4i fa[4], fb[2];
 #pragma unroll
-      for (int i = 0; i < 2; i++)
-        fa[i] = *(const v4i *)&As[buf][(wm * 64 + 32 * i + fr) * LS + 32 * s + fk];
+      for (int i = 0; i < 4; i++) {
+        const int row = wm * 128 + 32 * i + fr;
+        fa[i] = *(const v4i *)(st + row * BK + 16 * ((2 * s + fh) ^ swz(row)));
+      }
 #pragma unroll
-      for (int j = 0; j < 2; j++)
-        fb[j] = *(const v4i *)&Bs[buf][(wn * 64 + 32 * j + fr) * LS + 32 * s + fk];
+      for (int j = 0; j < 2; j++) {
+        const int row = wn * 64 + 32 * j + fr;
+        fb[j] = *(const v4i *)(st + A_BYTES + row * BK + 16 * ((2 * s + fh) ^ swz(row)));
+      }
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
     }
-    if (kt + 1 < nk) lstore(buf ^ 1);
-    __syncthreads();
   }
 
-  // ---- epilogue: lane holds column fr of each 32x32 block ----
+  // ---- epilogue ----
+  // Values are formed in the MFMA layout (lane: column fr, 16 rows per
+  // 32-row block), written to a per-wave LDS tile, and leave as 16-byte
+  // row segments (the residual of EPI_ACCUM is read the same way).
+  __syncthreads();  // the ring is no longer read: reuse it for the tiles
   const int nw = n0 + wn * 64;  // first column of the wave tile
   int ncol[2];
   float zc[2], sb[2];
@@ -107,17 +149,35 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     sb[j] = a.sb[ncol[j]];
     c128[j] = a.c128[ncol[j]];
   }
+  constexpr int LDT = 68;  // floats per LDS tile row (64 + 4 padding)
+  float *tile = (float *)(smem + wave * (32 * LDT * 4));
+  const bool vec = (a.ldc & 3) == 0;
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < 4; i++) {
+    const int rb = wm * 128 + 32 * i;  // first row of the block in the tile
+    // wave-uniform; a wave past M still meets both barriers below
+    const bool live = m0 + rb < a.M;
+    // RoPE tables of the block's 16 rows of this lane, gathered up front
+    float rc[16], rs[16];
+    if constexpr (EPI == EPI_ROPE) {
+      if (live && nw < a.rope_cols) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int m = m0 + wm * 64 + 32 * i + acc_row(r, lane);
-      if (m >= a.M) continue;
-      const float sa = a.sa[m];
+        for (int r = 0; r < 16; r++) {
+          const int p = pos_s[rb + acc_row(r, lane)];
+          rc[r] = a.rope_cos[(size_t)p * 32 + fr];
+          rs[r] = a.rope_sin[(size_t)p * 32 + fr];
+        }
+      }
+    }
+    // (1) MFMA layout -> LDS tile
+#pragma unroll
+    for (int r = 0; r < 16 && live; r++) {
+      const int rl = acc_row(r, lane);
+      const int m = min(m0 + rb + rl, a.M - 1);
+      const float sa = sa_s[rb + rl];
       if constexpr (EPI == EPI_TILE) {
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-          if (ncol[j] < a.n_valid) a.Ci[(size_t)m * a.ldc + ncol[j]] = acc[i][j][r] + c128[j];
+        tile[rl * LDT + fr] = __int_as_float(acc[i][0][r] + c128[0]);
+        tile[rl * LDT + 32 + fr] = __int_as_float(acc[i][1][r] + c128[1]);
       } else if constexpr (EPI == EPI_GEGLU) {
         // Columns nw..nw+31 hold the GELU input of gated columns
         // nw/2..nw/2+31, columns nw+32..nw+63 their multiplier
@@ -125,19 +185,15 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
         const float va = deq(acc[i][0][r] + c128[0], zc[0], sb[0], sa);
         const float vb = deq(acc[i][1][r] + c128[1], zc[1], sb[1], sa);
         const int gc = nw / 2 + fr;
-        if (gc < a.n_valid) {
-          const float ge = gc < a.n_gelu ? gelu_fma(va) : gelu_scalar(va);
-          a.C[(size_t)m * a.ldc + gc] = ge * vb;
-        }
+        const float ge = gc < a.n_gelu ? gelu_fma(va) : gelu_scalar(va);
+        tile[rl * LDT + fr] = ge * vb;
       } else if constexpr (EPI == EPI_ROPE) {
         float v0 = deq(acc[i][0][r] + c128[0], zc[0], sb[0], sa);
         float v1 = deq(acc[i][1][r] + c128[1], zc[1], sb[1], sa);
         if (nw < a.rope_cols) {
           // linalg.Rope (vec_simd.go:408-425) on the head whose 64 values
           // are this wave tile: x1' = x1*c - x2*s, x2' = x2*c + x1*s.
-          const int p = a.pos[m];
-          const float c = a.rope_cos[(size_t)p * 32 + fr];
-          const float s = a.rope_sin[(size_t)p * 32 + fr];
+          const float c = rc[r], s = rs[r];
           const float x1 = v0, x2 = v1;
           v0 = x1 * c - x2 * s;
           v1 = x2 * c + x1 * s;
@@ -154,28 +210,95 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
             sc = mx / 127.0f;
             inv = 1.0f / sc;
           }
-          int8_t *qrow = a.qq + (size_t)m * a.q_cols + nw;
-          qrow[fr] = (int8_t)q8(v0, inv);
-          qrow[32 + fr] = (int8_t)q8(v1, inv);
-          if (fr == 0) a.sq[(size_t)m * (a.q_cols / 64) + nw / 64] = sc * a.attn_scale;
-          continue;
+          int8_t *qt = (int8_t *)tile;
+          qt[rl * 64 + fr] = (int8_t)q8(v0, inv);
+          qt[rl * 64 + 32 + fr] = (int8_t)q8(v1, inv);
+          if (fr == 0 && m0 + rb + rl < a.M)
+            a.sq[(size_t)(m0 + rb + rl) * (a.q_cols / 64) + nw / 64] = sc * a.attn_scale;
+        } else {
+          tile[rl * LDT + fr] = v0;
+          tile[rl * LDT + 32 + fr] = v1;
         }
-        float *row = a.C + (size_t)m * a.ldc;
-        if (ncol[0] < a.n_valid) row[ncol[0]] = v0;
-        if (ncol[1] < a.n_valid) row[ncol[1]] = v1;
       } else {
-        float *row = a.C + (size_t)m * a.ldc;
+        tile[rl * LDT + fr] = deq(acc[i][0][r] + c128[0], zc[0], sb[0], sa);
+        tile[rl * LDT + 32 + fr] = deq(acc[i][1][r] + c128[1], zc[1], sb[1], sa);
+      }
+    }
+    __syncthreads();
+    // (2) LDS tile -> global, 16 bytes per lane
+    if (!live) {
+    } else if constexpr (EPI == EPI_GEGLU) {
+      // 32 rows x 32 gated columns: lane (row l/8 + 8u, columns 4*(l%8))
+      const int c4 = lane & 7, gc = nw / 2 + 4 * c4;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-          if (ncol[j] >= a.n_valid) continue;
-          const float v = deq(acc[i][j][r] + c128[j], zc[j], sb[j], sa);
-          if constexpr (EPI == EPI_ACCUM || EPI == EPI_ACCUM_MLP)
-            row[ncol[j]] = row[ncol[j]] + v;
+      for (int u = 0; u < 4; u++) {
+        const int rl = (lane >> 3) + 8 * u, m = m0 + rb + rl;
+        const float4 v = *(const float4 *)&tile[rl * LDT + 4 * c4];
+        if (m < a.M) {
+          float *dst = a.C + (size_t)m * a.ldc + gc;
+          if (vec && gc + 4 <= a.n_valid) {
+            *(float4 *)dst = v;
+          } else {
+            const float e[4] = {v.x, v.y, v.z, v.w};
+            for (int t = 0; t < 4; t++)
+              if (gc + t < a.n_valid) dst[t] = e[t];
+          }
+        }
+      }
+    } else if (EPI == EPI_ROPE && nw < a.q_cols) {
+      // 32 rows x 64 int8: lane (row l/4 + 16u, bytes 16*(l%4))
+      const int8_t *qt = (const int8_t *)tile;
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int rl = (lane >> 2) + 16 * u, m = m0 + rb + rl;
+        const v4i v = *(const v4i *)&qt[rl * 64 + 16 * (lane & 3)];
+        if (m < a.M) *(v4i *)(a.qq + (size_t)m * a.q_cols + nw + 16 * (lane & 3)) = v;
+      }
+    } else {
+      // 32 rows x 64 values: lane (row l/16 + 4u, columns 4*(l%16))
+      const int c4 = lane & 15, col = nw + 4 * c4;
+      float4 old[8];
+      if constexpr (EPI == EPI_ACCUM || EPI == EPI_ACCUM_MLP) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          const int m = min(m0 + rb + (lane >> 4) + 4 * u, a.M - 1);
+          if (vec && col + 4 <= a.n_valid)
+            old[u] = *(const float4 *)(a.C + (size_t)m * a.ldc + col);
           else
-            row[ncol[j]] = v;
+            old[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int rl = (lane >> 4) + 4 * u, m = m0 + rb + rl;
+        float4 v = *(const float4 *)&tile[rl * LDT + 4 * c4];
+        if (m >= a.M) continue;
+        if constexpr (EPI == EPI_TILE) {
+          int32_t *dst = a.Ci + (size_t)m * a.ldc + col;
+          const int e[4] = {__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z),
+                            __float_as_int(v.w)};
+          if (vec && col + 4 <= a.n_valid) {
+            *(int4 *)dst = make_int4(e[0], e[1], e[2], e[3]);
+          } else {
+            for (int t = 0; t < 4; t++)
+              if (col + t < a.n_valid) dst[t] = e[t];
+          }
+        } else {
+          float *dst = a.C + (size_t)m * a.ldc + col;
+          const bool acc_in = EPI == EPI_ACCUM || EPI == EPI_ACCUM_MLP;
+          if (vec && col + 4 <= a.n_valid) {
+            if (acc_in)
+              v = make_float4(old[u].x + v.x, old[u].y + v.y, old[u].z + v.z, old[u].w + v.w);
+            *(float4 *)dst = v;
+          } else {
+            const float e[4] = {v.x, v.y, v.z, v.w};
+            for (int t = 0; t < 4; t++)
+              if (col + t < a.n_valid) dst[t] = acc_in ? dst[t] + e[t] : e[t];
+          }
         }
       }
     }
+    __syncthreads();
   }
 }
 
@@ -183,15 +306,28 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
 
 void launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
   if (a.M <= 0) return;
-  const int mt = (a.M + BM - 1) / BM, nt = a.Np / BN;
-  dim3 grid(mt * nt), block(256);
+  const int tiles = ((a.M + BM - 1) / BM) * (a.Np / BN);
+  const int per_xcd = (tiles + NXCD - 1) / NXCD;
+  dim3 grid(per_xcd * NXCD), block(256);
+  const size_t shm = (size_t)STAGES * STAGE_BYTES;
+  // 72 KB of LDS per workgroup (gfx950 has 160 KB per CU): allow more than
+  // the default 64 KB of dynamic LDS, once per kernel instance.
+  static bool attr_set[6] = {};
+  auto launch = [&](auto kern) {
+    if (!attr_set[epi]) {
+      (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)shm);
+      attr_set[epi] = true;
+    }
+    kern<<<grid, block, shm, s>>>(a);
+  };
   switch (epi) {
-  case EPI_STORE: gemm_i8_kernel<EPI_STORE><<<grid, block, 0, s>>>(a); break;
-  case EPI_ACCUM: gemm_i8_kernel<EPI_ACCUM><<<grid, block, 0, s>>>(a); break;
-  case EPI_TILE: gemm_i8_kernel<EPI_TILE><<<grid, block, 0, s>>>(a); break;
-  case EPI_GEGLU: gemm_i8_kernel<EPI_GEGLU><<<grid, block, 0, s>>>(a); break;
-  case EPI_ROPE: gemm_i8_kernel<EPI_ROPE><<<grid, block, 0, s>>>(a); break;
-  case EPI_ACCUM_MLP: gemm_i8_kernel<EPI_ACCUM_MLP><<<grid, block, 0, s>>>(a); break;
+  case EPI_STORE: launch(gemm_i8_kernel<EPI_STORE>); break;
+  case EPI_ACCUM: launch(gemm_i8_kernel<EPI_ACCUM>); break;
+  case EPI_TILE: launch(gemm_i8_kernel<EPI_TILE>); break;
+  case EPI_GEGLU: launch(gemm_i8_kernel<EPI_GEGLU>); break;
+  case EPI_ROPE: launch(gemm_i8_kernel<EPI_ROPE>); break;
+  case EPI_ACCUM_MLP: launch(gemm_i8_kernel<EPI_ACCUM_MLP>); break;
   }
 }
 
