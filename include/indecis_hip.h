@@ -187,6 +187,18 @@ int ixh_attend8(int device, float *o, const float *q, const float *k,
                 const float *v, int n, int d, int window, float scale,
                 int lanes);
 
+/* Self-check of the attention kernels' softmax rounding (no counterpart in
+ * the reference; for tests and deployment checks). The kernels round
+ * 255*exp(s - max) with the device's base-2 exponential and fall back to
+ * the reference's exp32 formulas where the value is within a tolerance of
+ * a rounding boundary. For every float v in [-inf, -0] and +0 this counts
+ * the v where that shortcut would round differently from the reference:
+ * bad[0] for the vector formula (ExpShift's SIMD body), bad[1] for the
+ * scalar exp32; both must be 0. max_err[0..1]: the largest distance of the
+ * shortcut from 255*exp(v) of each formula; *undecided: how many v take the
+ * fallback. */
+int ixh_check_exp255(int device, int64_t bad[2], float max_err[2], int64_t *undecided);
+
 #ifdef __cplusplus
 }
 #endif

@@ -201,12 +201,11 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
   const int V = a.lanes;
   const int ts = V > 0 ? cs + ((ce - cs) / V) * V : cs;
   // wave-wide bounds over the active queries: a tile [k0, k0+32) with
-  // k0 >= cs_hi and k0+32 <= ts_lo is valid and exp-vector for every query
-  int cs_hi = qact ? cs : 0, ts_lo = qact ? ts : 1 << 30, ce_hi = qact ? ce : 0;
+  // k0 >= cs_hi and k0+32 <= ce_lo is valid for every query
+  int cs_hi = qact ? cs : 0, ce_lo = qact ? ce : 1 << 30;
   for (int t = 1; t < 64; t <<= 1) {
     cs_hi = max(cs_hi, __shfl_xor(cs_hi, t));
-    ts_lo = min(ts_lo, __shfl_xor(ts_lo, t));
-    ce_hi = max(ce_hi, __shfl_xor(ce_hi, t));
+    ce_lo = min(ce_lo, __shfl_xor(ce_lo, t));
   }
 
   // key tiles (32 keys) of this wave and of the block
@@ -259,8 +258,9 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
       *(v4i *)&Vs[d * VS + 32 * g + 16] = o1;
     }
   };
-  // Scores of tile t: ((f32(sum q*k)) * ks) * sq, in the S^T layout (rows
-  // = keys 8*(r/4) + 4*(lane/32) + r%4 of the tile, column = this query).
+  // Scores of tile t without the query scale: f32(sum q*k) * ks, in the S^T
+  // layout (rows = keys 8*(r/4) + 4*(lane/32) + r%4 of the tile, column =
+  // this query). The score is that times sq.
   auto scores = [&](int t, int c0, float *sv) {
     v16i acc;
 #pragma unroll
@@ -272,14 +272,16 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
 #pragma unroll
     for (int g = 0; g < 4; g++) {
       const float4 k4 = *(const float4 *)(kt + 8 * g);
-      sv[4 * g] = ((float)acc[4 * g] * k4.x) * sqv;
-      sv[4 * g + 1] = ((float)acc[4 * g + 1] * k4.y) * sqv;
-      sv[4 * g + 2] = ((float)acc[4 * g + 2] * k4.z) * sqv;
-      sv[4 * g + 3] = ((float)acc[4 * g + 3] * k4.w) * sqv;
+      sv[4 * g] = (float)acc[4 * g] * k4.x;
+      sv[4 * g + 1] = (float)acc[4 * g + 1] * k4.y;
+      sv[4 * g + 2] = (float)acc[4 * g + 2] * k4.z;
+      sv[4 * g + 3] = (float)acc[4 * g + 3] * k4.w;
     }
   };
 
   // ---- pass 1: row max of the valid scores ----
+  // max_j f32(x_j * sq) = f32(max_j x_j * sq): rounding is monotone and
+  // sq >= 0, so the query scale is applied once, to the max.
   float m = -__builtin_huge_valf();
   for (int c0 = bk0; c0 < bk1; c0 += CHUNK) {
     __syncthreads();
@@ -291,7 +293,7 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
       float sv[16];
       scores(t, c0, sv);
       const int k0 = t * 32;
-      if (k0 >= cs_hi && k0 + 32 <= ts_lo) {  // every key valid for every query
+      if (k0 >= cs_hi && k0 + 32 <= ce_lo) {  // every key valid for every query
 #pragma unroll
         for (int r = 0; r < 16; r++) m = fmax32(m, sv[r]);
       } else {
@@ -303,9 +305,13 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
       }
     }
   }
-  m = fmax32(m, __shfl_xor(m, 32));
+  m = fmax32(m, __shfl_xor(m, 32)) * sqv;
 
   // ---- pass 2: P = RNE(255 exp(s - m)), O^T += V^T . P^T ----
+  // P is rounded from the hardware exponential (exp255_fast) unless that
+  // lands within kExp255Tol of a half-integer; there (about 1 score in 500)
+  // the reference formula decides: exp32 on the tail keys j >= ts (all keys
+  // when lanes = 0), ExpShift's vector formula elsewhere.
   v16i ohi[2], olo[2];
 #pragma unroll
   for (int dt = 0; dt < 2; dt++)
@@ -324,25 +330,40 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
       float sv[16];
       scores(t, c0, sv);
       const int k0 = t * 32;
-      const bool full = k0 >= cs_hi && k0 + 32 <= ts_lo;
-      const bool tail = k0 + 32 > ts_lo && k0 < ce_hi;  // some exp32 tail key here
+      const bool full = k0 >= cs_hi && k0 + 32 <= ce_lo;  // every key valid for every query
+      float p[16];
+      unsigned undecided = 0;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        sv[r] = sv[r] * sqv - m;  // s - max, as the reference forms it
+        const float y = exp255_fast(sv[r]);
+        p[r] = rne(y);
+        undecided |= (fabsf(y - p[r]) > 0.5f - kExp255Tol) ? 1u << r : 0u;
+      }
+      if (undecided) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          if (undecided & (1u << r)) {
+            const int j = k0 + acc_row(r, lane);
+            const float e = (j >= ts) ? exp32_scalar(sv[r]) : exp32_simd(sv[r]);
+            // QuantizeRowU8 (vec_simd.go:64-91): RNE(e*255) in [0, 255]
+            p[r] = rne(e * 255.0f);
+          }
+        }
+      }
+      if (!full) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int j = k0 + acc_row(r, lane);
+          p[r] = (j >= cs && j < ce) ? p[r] : 0.0f;
+        }
+      }
       unsigned pw[4];
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         unsigned w = 0;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const int r = 4 * g + u;
-          const float v = sv[r] - m;
-          float e = exp32_simd(v);
-          if (!full) {
-            const int j = k0 + acc_row(r, lane);
-            if (tail) e = (j >= ts) ? exp32_scalar(v) : e;
-            e = (j >= cs && j < ce) ? e : 0.0f;
-          }
-          // QuantizeRowU8 (vec_simd.go:64-91): RNE(e*255) in [0, 255]
-          w = __builtin_amdgcn_cvt_pk_u8_f32(rne(e * 255.0f), u, w);
-        }
+        for (int u = 0; u < 4; u++) w = __builtin_amdgcn_cvt_pk_u8_f32(p[4 * g + u], u, w);
         pw[g] = w;
         psum = __builtin_amdgcn_udot4(w, 0x01010101u, psum, false);
       }
@@ -383,7 +404,54 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
   }
 }
 
+// Every float v = bits -> float over [lo, hi) (v <= 0 expected): counts
+// the v where exp255_fast decides the rounding (away from a half-integer by
+// more than kExp255Tol) and RNE differs from the reference's
+// RNE(f32(255*exp(v))), for exp32_simd (res[0]) and exp32_scalar (res[1]);
+// res[2], res[3]: largest |exp255_fast - 255*exp| of each formula, as
+// float bits; res[4]: number of undecided v.
+__global__ __launch_bounds__(256) void check_exp255_kernel(uint32_t lo, uint32_t hi,
+                                                           unsigned long long *res) {
+  unsigned long long bad_v = 0, bad_s = 0, amb = 0;
+  float err_v = 0.f, err_s = 0.f;
+  const uint32_t stride = gridDim.x * 256u;
+  for (uint32_t u = lo + blockIdx.x * 256u + threadIdx.x; u < hi && u >= lo; u += stride) {
+    const float v = __uint_as_float(u);
+    const float y = exp255_fast(v);
+    const float p = rne(y);
+    const bool decided = fabsf(y - p) <= 0.5f - kExp255Tol;
+    const float yv = exp32_simd(v) * 255.0f, ys = exp32_scalar(v) * 255.0f;
+    err_v = fmax32(err_v, fabsf(y - yv));
+    err_s = fmax32(err_s, fabsf(y - ys));
+    if (decided) {
+      bad_v += rne(yv) != p;
+      bad_s += rne(ys) != p;
+    } else {
+      amb++;
+    }
+  }
+  for (int t = 1; t < 64; t <<= 1) {
+    bad_v += __shfl_xor(bad_v, t);
+    bad_s += __shfl_xor(bad_s, t);
+    amb += __shfl_xor(amb, t);
+    err_v = fmax32(err_v, __shfl_xor(err_v, t));
+    err_s = fmax32(err_s, __shfl_xor(err_s, t));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(&res[0], bad_v);
+    atomicAdd(&res[1], bad_s);
+    atomicMax(&res[2], (unsigned long long)__float_as_uint(err_v));
+    atomicMax(&res[3], (unsigned long long)__float_as_uint(err_s));
+    atomicAdd(&res[4], amb);
+  }
+}
+
 }  // namespace
+
+void launch_check_exp255(uint32_t lo, uint32_t hi, unsigned long long *res, hipStream_t s) {
+  if (hi <= lo) return;
+  check_exp255_kernel<<<4096, 256, 0, s>>>(lo, hi, res);
+}
 
 void launch_attn_quant_q(const AttnArgs &a, hipStream_t s) {
   const long groups = (long)a.N * a.nh;

@@ -9,14 +9,19 @@
 // rescales it with the same float32 operations in the same order:
 // ((f32(tile) - zc[n]) * sb[n]) * sa[m] (+ C).
 //
-// Block tile 256x128, K step 64, 256 threads: 4 waves (2x2), each a 128x64
-// tile of 4x2 MFMA 32x32 blocks (128 accumulators). A and B stream into a
-// 3-stage LDS ring with direct-to-LDS loads (global_load_lds_dwordx4: a
+// Block tile (64*MI)x128, K step 64, 256 threads: 4 waves (2x2), each a
+// (32*MI)x64 tile of MIx2 MFMA 32x32 blocks. A and B stream into an
+// ST-stage LDS ring with direct-to-LDS loads (global_load_lds_dwordx4: a
 // wave instruction fills 1 KB, 16 rows of 64 bytes); the 16-byte chunks of
 // a row are XOR-swizzled by (row >> 1) & 3 so the 16-byte fragment reads of
 // consecutive rows fall in distinct banks. One barrier per K step; loads
-// run two K steps ahead. Tiles are handed out XCD by XCD so the N-tiles of
-// an A panel share one L2.
+// run ST-1 K steps ahead. Tiles are handed out XCD by XCD so the N-tiles of
+// an A panel share one L2. The default is 128x128 with 2 stages: 35 KB of
+// LDS and ~100 VGPRs let 4 workgroups share a CU, so one workgroup's
+// epilogue stores overlap the others' MFMA loops (on the encoder's shapes
+// it beats 256x128 tiles by 8-22%).
+#include <stdlib.h>
+
 #include "ixh_device.h"
 #include "ixh_internal.h"
 
@@ -24,9 +29,17 @@ namespace ixh {
 
 namespace {
 
-constexpr int BM = 256, BN = 128, BK = 64, STAGES = 3;
-constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK, STAGE_BYTES = A_BYTES + B_BYTES;
-constexpr int NXCD = 8;
+constexpr int BN = 128, BK = 64, NXCD = 8;
+constexpr int EPI_TILE_BYTES = 4 * 32 * 68 * 4;  // epilogue LDS tiles of the 4 waves
+
+// Tile configurations: MI 32-row MFMA blocks per wave (block tile BM = 64*MI
+// rows x 128 columns) and ST stages in the LDS ring.
+template <int MI, int ST>
+struct Cfg {
+  static constexpr int BM = 64 * MI, LOADS = MI + 2;  // direct-to-LDS loads per wave per stage
+  static constexpr int A_BYTES = BM * BK, STAGE_BYTES = (BM + BN) * BK;
+  static constexpr int SMEM = ST * STAGE_BYTES > EPI_TILE_BYTES ? ST * STAGE_BYTES : EPI_TILE_BYTES;
+};
 
 typedef __attribute__((address_space(3))) void *lds_ptr;
 typedef const __attribute__((address_space(1))) void *glb_ptr;
@@ -39,9 +52,21 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
+// wait until at most `stages` later stages (of L loads each) are in flight
+template <int L>
+__device__ __forceinline__ void wait_stages(int stages) {
+  if (stages >= 2)
+    wait_vmcnt<2 * L>();
+  else if (stages == 1)
+    wait_vmcnt<L>();
+  else
+    wait_vmcnt<0>();
+}
 
-template <int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
+template <int EPI, int MI, int ST>
+__global__ __launch_bounds__(256, MI == 4 ? 2 : 3) void gemm_i8_kernel(GemmArgs a) {
+  using C = Cfg<MI, ST>;
+  constexpr int BM = C::BM, A_BYTES = C::A_BYTES, STAGE_BYTES = C::STAGE_BYTES;
   extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -55,16 +80,16 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
   const int nt = tix % ntn, mt = tix / ntn;
   const int m0 = mt * BM, n0 = nt * BN;
 
-  // This wave's direct-to-LDS loads of a stage: A chunks 4*wave..+3 (rows
-  // 64*wave + 16u + lane/4), B chunks 2*wave..+1 (rows 32*wave + 16u +
-  // lane/4). Lane i fills LDS bytes 16i of its chunk: row i/4, physical
-  // 16-byte column i%4, i.e. logical column (i%4) ^ swz(row).
+  // This wave's direct-to-LDS loads of a stage: A chunks MI*wave..+MI-1
+  // (rows 16*MI*wave + 16u + lane/4), B chunks 2*wave..+1 (rows 32*wave +
+  // 16u + lane/4). Lane i fills LDS bytes 16i of its chunk: row i/4,
+  // physical 16-byte column i%4, i.e. logical column (i%4) ^ swz(row).
   const int lrow = lane >> 2, lchunk = (lane & 3) ^ swz(lane >> 2);
-  glb_ptr ag[4];
+  glb_ptr ag[MI];
   glb_ptr bg[2];
 #pragma unroll
-  for (int u = 0; u < 4; u++) {
-    int row = m0 + 64 * wave + 16 * u + lrow;
+  for (int u = 0; u < MI; u++) {
+    int row = m0 + 16 * MI * wave + 16 * u + lrow;
     row = row < a.M ? row : a.M - 1;  // rows past M load row M-1 (never stored)
     ag[u] = (glb_ptr)(a.A + (size_t)row * a.lda + 16 * lchunk);
   }
@@ -73,21 +98,21 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
     bg[u] = (glb_ptr)(a.B + (size_t)(n0 + 32 * wave + 16 * u + lrow) * a.ldb + 16 * lchunk);
 
   auto issue = [&](int kt) {
-    int8_t *st = smem + (kt % STAGES) * STAGE_BYTES;
+    int8_t *st = smem + (kt % ST) * STAGE_BYTES;
     const int k0 = kt * BK;
 #pragma unroll
-    for (int u = 0; u < 4; u++)
+    for (int u = 0; u < MI; u++)
       __builtin_amdgcn_global_load_lds((glb_ptr)((const int8_t *)ag[u] + k0),
-                                       (lds_ptr)(st + (64 * wave + 16 * u) * BK), 16, 0, 0);
+                                       (lds_ptr)(st + (16 * MI * wave + 16 * u) * BK), 16, 0, 0);
 #pragma unroll
     for (int u = 0; u < 2; u++)
       __builtin_amdgcn_global_load_lds((glb_ptr)((const int8_t *)bg[u] + k0),
                                        (lds_ptr)(st + A_BYTES + (32 * wave + 16 * u) * BK), 16, 0, 0);
   };
 
-  v16i acc[4][2];
+  v16i acc[MI][2];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < MI; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -95,30 +120,31 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
 
   // per-row activation scales of the tile, for the epilogue
   __shared__ float sa_s[BM];
-  sa_s[tid] = a.sa[min(m0 + tid, a.M - 1)];
   __shared__ int pos_s[EPI == EPI_ROPE ? BM : 1];
-  if constexpr (EPI == EPI_ROPE) pos_s[tid] = a.pos[min(m0 + tid, a.M - 1)];
+  if (tid < BM) {
+    sa_s[tid] = a.sa[min(m0 + tid, a.M - 1)];
+    if constexpr (EPI == EPI_ROPE) pos_s[tid] = a.pos[min(m0 + tid, a.M - 1)];
+  }
 
   const int nk = a.Kp / BK;
   const int fr = lane & 31, fh = lane >> 5;
-  issue(0);
-  if (nk > 1) issue(1);
+#pragma unroll
+  for (int p = 0; p < ST - 1; p++)
+    if (p < nk) issue(p);
   for (int kt = 0; kt < nk; kt++) {
-    if (kt + 1 < nk)
-      wait_vmcnt<6>();  // this K step's 6 loads done, the next step's in flight
-    else
-      wait_vmcnt<0>();
-    // every wave's loads landed; stage (kt+2)%3 is free. A bare s_barrier:
-    // __syncthreads' fence would also drain the next stage's loads.
+    // this K step's loads done, the next ST-2 steps' may be in flight
+    wait_stages<C::LOADS>(min(ST - 2, nk - 1 - kt));
+    // every wave's loads landed; stage (kt+ST-1)%ST is free. A bare
+    // s_barrier: __syncthreads' fence would also drain the next loads.
     __builtin_amdgcn_s_barrier();
-    if (kt + 2 < nk) issue(kt + 2);
-    const int8_t *st = smem + (kt % STAGES) * STAGE_BYTES;
+    if (kt + ST - 1 < nk) issue(kt + ST - 1);
+    const int8_t *st = smem + (kt % ST) * STAGE_BYTES;
 #pragma unroll
     for (int s = 0; s < 2; s++) {
-      v4i fa[4], fb[2];
+      v4i fa[MI], fb[2];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int row = wm * 128 + 32 * i + fr;
+      for (int i = 0; i < MI; i++) {
+        const int row = wm * 32 * MI + 32 * i + fr;
         fa[i] = *(const v4i *)(st + row * BK + 16 * ((2 * s + fh) ^ swz(row)));
       }
 #pragma unroll
@@ -127,7 +153,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
         fb[j] = *(const v4i *)(st + A_BYTES + row * BK + 16 * ((2 * s + fh) ^ swz(row)));
       }
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
     }
@@ -153,8 +179,8 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
   float *tile = (float *)(smem + wave * (32 * LDT * 4));
   const bool vec = (a.ldc & 3) == 0;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int rb = wm * 128 + 32 * i;  // first row of the block in the tile
+  for (int i = 0; i < MI; i++) {
+    const int rb = wm * 32 * MI + 32 * i;  // first row of the block in the tile
     // wave-uniform; a wave past M still meets both barriers below
     const bool live = m0 + rb < a.M;
     // RoPE tables of the block's 16 rows of this lane, gathered up front
@@ -304,15 +330,18 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
 
 }  // namespace
 
-void launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
-  if (a.M <= 0) return;
-  const int tiles = ((a.M + BM - 1) / BM) * (a.Np / BN);
+namespace {
+
+template <int MI, int ST>
+void launch_cfg(int epi, const GemmArgs &a, hipStream_t s) {
+  using C = Cfg<MI, ST>;
+  const int tiles = ((a.M + C::BM - 1) / C::BM) * (a.Np / BN);
   const int per_xcd = (tiles + NXCD - 1) / NXCD;
-  dim3 grid(per_xcd * NXCD), block(256);
-  const size_t shm = (size_t)STAGES * STAGE_BYTES;
-  // 72 KB of LDS per workgroup (gfx950 has 160 KB per CU): allow more than
-  // the default 64 KB of dynamic LDS, once per kernel instance.
-  static bool attr_set[6] = {};
+  const dim3 grid(per_xcd * NXCD), block(256);
+  const size_t shm = C::SMEM;
+  // up to 72 KB of LDS per workgroup (gfx950 has 160 KB per CU): allow more
+  // than the default 64 KB of dynamic LDS, once per kernel instance
+  static bool attr_set[8] = {};
   auto launch = [&](auto kern) {
     if (!attr_set[epi]) {
       (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -322,12 +351,29 @@ void launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
     kern<<<grid, block, shm, s>>>(a);
   };
   switch (epi) {
-  case EPI_STORE: launch(gemm_i8_kernel<EPI_STORE>); break;
-  case EPI_ACCUM: launch(gemm_i8_kernel<EPI_ACCUM>); break;
-  case EPI_TILE: launch(gemm_i8_kernel<EPI_TILE>); break;
-  case EPI_GEGLU: launch(gemm_i8_kernel<EPI_GEGLU>); break;
-  case EPI_ROPE: launch(gemm_i8_kernel<EPI_ROPE>); break;
-  case EPI_ACCUM_MLP: launch(gemm_i8_kernel<EPI_ACCUM_MLP>); break;
+  case EPI_STORE: launch(gemm_i8_kernel<EPI_STORE, MI, ST>); break;
+  case EPI_ACCUM: launch(gemm_i8_kernel<EPI_ACCUM, MI, ST>); break;
+  case EPI_TILE: launch(gemm_i8_kernel<EPI_TILE, MI, ST>); break;
+  case EPI_GEGLU: launch(gemm_i8_kernel<EPI_GEGLU, MI, ST>); break;
+  case EPI_ROPE: launch(gemm_i8_kernel<EPI_ROPE, MI, ST>); break;
+  case EPI_ACCUM_MLP: launch(gemm_i8_kernel<EPI_ACCUM_MLP, MI, ST>); break;
+  }
+}
+
+}  // namespace
+
+void launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
+  if (a.M <= 0) return;
+  int cfg = a.tile_cfg;
+  if (cfg == 0) {
+    // IXH_GEMM_TILE=1|2 selects another tile configuration (tuning and tests)
+    const char *e = getenv("IXH_GEMM_TILE");
+    if (e) cfg = atoi(e);
+  }
+  switch (cfg) {
+  case 1: launch_cfg<4, 3>(epi, a, s); break;
+  case 2: launch_cfg<2, 3>(epi, a, s); break;
+  default: launch_cfg<2, 2>(epi, a, s); break;
   }
 }
 

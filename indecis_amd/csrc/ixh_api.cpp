@@ -1256,4 +1256,30 @@ int ixh_attend8(int device, float *o, const float *q, const float *k, const floa
   return IXH_OK;
 }
 
+
+int ixh_check_exp255(int device, int64_t bad[2], float max_err[2], int64_t *undecided) {
+  if (!bad || !max_err || !undecided) return fail(IXH_EINVAL, "linalg: hip: nil result");
+  DEVGUARD(device);
+  TmpStream ts;
+  HIPCK(hipStreamCreateWithFlags(&ts.s, hipStreamNonBlocking));
+  DevBuf dres;
+  int rc;
+  if ((rc = dres.ensure(5 * sizeof(unsigned long long)))) return rc;
+  HIPCK(hipMemsetAsync(dres.p, 0, 5 * sizeof(unsigned long long), ts.s));
+  // +0, then -0 .. -inf (sign bit set, exponent and mantissa up to 0x7f800000)
+  launch_check_exp255(0u, 1u, dres.as<unsigned long long>(), ts.s);
+  launch_check_exp255(0x80000000u, 0xff800001u, dres.as<unsigned long long>(), ts.s);
+  LAUNCHCK("check_exp255");
+  unsigned long long r[5];
+  HIPCK(hipMemcpyAsync(r, dres.p, sizeof r, hipMemcpyDeviceToHost, ts.s));
+  HIPCK(hipStreamSynchronize(ts.s));
+  bad[0] = (int64_t)r[0];
+  bad[1] = (int64_t)r[1];
+  uint32_t e0 = (uint32_t)r[2], e1 = (uint32_t)r[3];
+  memcpy(&max_err[0], &e0, 4);
+  memcpy(&max_err[1], &e1, 4);
+  *undecided = (int64_t)r[4];
+  return IXH_OK;
+}
+
 }  // extern "C"

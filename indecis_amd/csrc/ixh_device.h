@@ -69,6 +69,17 @@ __device__ __forceinline__ float exp32_simd(float v) {
   return under ? 0.0f : y * pw;
 }
 
+// 255*exp(v) from the hardware base-2 exponential (v_exp_f32): fma(v,
+// log2 e, log2 255), then 2^x. Used only to round: where it lies more than
+// kExp255Tol from a half-integer, RNE of it equals RNE(f32(255*exp32(v)))
+// for both reference formulas (exp32_simd and exp32_scalar), for every
+// float v <= 0 — ixh_check_exp255 verifies this on the device, float by
+// float. Elsewhere the caller evaluates the reference formula.
+constexpr float kExp255Tol = 1.0f / 1024;
+__device__ __forceinline__ float exp255_fast(float v) {
+  return __builtin_amdgcn_exp2f(__builtin_fmaf(v, 1.44269504088896341f, 7.99435343685885793f));
+}
+
 // GELU (erf) of geluMulAVX2 (linalg/gelu_amd64.s:173-195).
 __device__ __forceinline__ float gelu_fma(float x) {
   float t = x * 0.7071067811865476f;

@@ -46,6 +46,7 @@ struct GemmArgs {
   int8_t *qq;
   float *sq;
   float attn_scale;
+  int tile_cfg;  // 0: 128x128 tiles, 2 LDS stages; 1: 256x128, 3; 2: 128x128, 3
 };
 
 void launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
@@ -114,6 +115,10 @@ struct AttnArgs {
 void launch_attn_quant_q(const AttnArgs &a, hipStream_t s);
 void launch_attn_prologue(const AttnArgs &a, hipStream_t s);
 void launch_attn_main(const AttnArgs &a, hipStream_t s);
+// exp255_fast against the reference exponentials over float bits [lo, hi):
+// res[5] (zeroed by the caller) = {bad simd, bad scalar, max err simd bits,
+// max err scalar bits, undecided}
+void launch_check_exp255(uint32_t lo, uint32_t hi, unsigned long long *res, hipStream_t s);
 
 constexpr int kAttnQBlock = 128;  // queries per workgroup (4 waves x 32)
 constexpr int kKeyPad = 64;       // key slots of a sequence are padded to this

@@ -101,3 +101,14 @@ def attend8(q, k, v, window=-1, scale=0.125, lanes=8, device=0):
     _lib.check(_lib.lib().ixh_attend8(device, _ptr(o), _ptr(q), _ptr(k), _ptr(v), n, d, window,
                                       float(scale), lanes))
     return o[:n]
+
+
+def check_exp255(device=0):
+    """Runs the device self-check of the attention softmax rounding over
+    every float v <= 0: returns (bad_simd, bad_scalar, max_err_simd,
+    max_err_scalar, undecided). bad_* must be 0."""
+    bad = (C.c_int64 * 2)()
+    err = (C.c_float * 2)()
+    und = C.c_int64()
+    _lib.check(_lib.lib().ixh_check_exp255(device, bad, err, C.byref(und)))
+    return int(bad[0]), int(bad[1]), float(err[0]), float(err[1]), int(und.value)

@@ -4,8 +4,9 @@ outputs bit-exact (the kernels reproduce the reference's roundings)."""
 import numpy as np
 import pytest
 
-from helpers import f32_bits_equal, mismatch_report
+from helpers import f32_bits_equal, ids_uniform_lengths, mismatch_report, small_cfg
 from indecis_amd import linalg
+from indecis_amd.modernbert import Model, Weights
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -126,3 +127,45 @@ def test_attend8_exact(n, window, lanes):
     ref = orc.attend8(q, k, v, window, 0.125, lanes)
     o = linalg.attend8(q, k, v, window, 0.125, lanes)
     assert f32_bits_equal(o, ref), mismatch_report(o, ref)
+
+
+@pytest.mark.parametrize("tile_cfg", ["1", "2"])
+def test_gemm_tile_configs(tile_cfg, monkeypatch):
+    """The 256x128 / 3-stage and 128x128 / 3-stage tile configurations
+    (IXH_GEMM_TILE) give the same reference tile and floats as the default,
+    on ragged shapes that leave partial M tiles and padded N and K."""
+    monkeypatch.setenv("IXH_GEMM_TILE", tile_cfg)
+    rng = np.random.default_rng(int(tile_cfg))
+    for m, k, n in [(7, 384, 1152), (257, 70, 40), (300, 1152, 768), (1000, 768, 2304)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        q, s = _weights(rng, n, k)
+        b = linalg.PackedB8(q, s)
+        aq, sa, tile = linalg.matmul8_tile(a, b)
+        aq_ref, sa_ref = orc.quantize_rows(a)
+        assert np.array_equal(tile, orc.matmul8_tile(aq_ref, q))
+        c0 = rng.standard_normal((m, n)).astype(np.float32)
+        colsum = q.astype(np.int32).sum(axis=1).astype(np.int32)
+        ref = orc.matmul8(a, q, s, colsum, c=c0, accumulate=True)
+        got = linalg.matmul8(c0.copy(), a, b, m, accumulate=True)
+        assert f32_bits_equal(got, ref), mismatch_report(got, ref)
+    # the whole encoder (RoPE/Q-quant, GeGLU and residual epilogues)
+    cfg = small_cfg()
+    w = Weights.random(cfg, seed=5)
+    gpu, ora = Model(w, lanes=8), orc.OracleModel(w, lanes=8)
+    seqs = ids_uniform_lengths(rng, 5, 1, 300, cfg.vocab)
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    gpu.close()
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+
+
+def test_exp255_shortcut_every_float():
+    """The attention kernels round 255*exp(v) from the hardware exponential
+    and fall back to the reference formulas (ExpShift's vector body and
+    exp32, vec_simd.go:235-262) only near a rounding boundary. Over every
+    float v <= 0 the shortcut must never round differently from either
+    formula; its distance from them stays far below the margin."""
+    bad_v, bad_s, err_v, err_s, undecided = linalg.check_exp255()
+    assert bad_v == 0 and bad_s == 0, (bad_v, bad_s)
+    assert err_v < 2e-4 and err_s < 2e-4, (err_v, err_s)
+    print(f"max |fast - ref|: simd {err_v:.3g}, scalar {err_s:.3g}; undecided floats {undecided}")
