@@ -51,7 +51,8 @@ __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
 __global__ __launch_bounds__(256) void attn_prologue_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float kst[64 * D];
   __shared__ float vmaxp[16][D];
-  __shared__ float mean[D], vinv[D];
+  __shared__ __attribute__((aligned(16))) float mean[D];
+  __shared__ __attribute__((aligned(16))) float vinv[D];
   __shared__ __attribute__((aligned(16))) int8_t vtile[D][64 + 16];
   const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const int sub = tid & 15, rg = tid >> 4;
@@ -145,6 +146,144 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(AttnArgs a) {
       *(v4i *)(vt + (size_t)d * a.Npad + c0 + 16 * seg) = *(const v4i *)&vtile[d][16 * seg];
     }
     __syncthreads();
+  }
+}
+
+// Single-read prologue for sequences of at most kShortSeq keys: one
+// workgroup of 512 threads per (sequence, head, K or V) holds the
+// sequence's 64-wide head slice in registers (16 float4 per thread), so K
+// and V are read from HBM once.
+//  K (blockIdx.z 0): row j = rg + 32u (rg = tid/16, u < 16). The 64
+//    sequential float32 chains of the mean run in wave 0 over 32-row pieces
+//    written to a double-buffered LDS slab (one barrier per piece); then
+//    each row is centred and quantised from registers.
+//  V (blockIdx.z 1): row j = 16 rg + u, so a thread holds 16 consecutive
+//    keys of 4 dimensions: max |V| per dimension by a block reduction, then
+//    each dimension's 16 quantised keys leave as one 16-byte store into
+//    V^T.
+constexpr int kShortSeq = 512;
+__global__ __launch_bounds__(512, 4) void attn_prologue_short_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float kst[2][32 * D];
+  __shared__ __attribute__((aligned(16))) float red[8][D];
+  __shared__ __attribute__((aligned(16))) float mean[D];
+  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int sub = tid & 15, rg = tid >> 4, wave = tid >> 6, lane = tid & 63;
+  const int base = a.offs[b], n = a.offs[b + 1] - base;
+  const int slot0 = a.padoff[b];
+  const int npad = (n + kKeyPad - 1) / kKeyPad * kKeyPad;
+  const int H = a.H, ld = 3 * H;
+  // the sequence's rows of qkv; a row is 4*ld bytes
+  const __amdgpu_buffer_rsrc_t rows = buf_rsrc(a.qkv + (size_t)base * ld, (uint32_t)n * ld * 4);
+  const uint32_t col = 4u * (H + h * D + 4 * sub);  // byte offset of this thread's K float4
+  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+
+  if (blockIdx.z == 0) {
+    float4 kr[16];
+    const uint32_t voff = (uint32_t)rg * ld * 4 + col;
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      const int j = rg + 32 * u;
+      kr[u] = j < n ? buf_load_f4(rows, voff, (uint32_t)(32 * u) * ld * 4) : zero4;
+    }
+    // sum of K in key order (AddTo, attention8.go:224-228)
+    float ksum = 0.f;
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      if (32 * u < n) {  // block-uniform
+        *(float4 *)&kst[u & 1][rg * D + 4 * sub] = kr[u];
+        __syncthreads();
+        if (wave == 0) {
+          const float *col = &kst[u & 1][lane];
+          const int cnt = min(32, n - 32 * u);
+          if (cnt == 32) {
+#pragma unroll
+            for (int rr = 0; rr < 32; rr++) ksum = ksum + col[rr * D];
+          } else {
+            for (int rr = 0; rr < cnt; rr++) ksum = ksum + col[rr * D];
+          }
+        }
+      }
+    }
+    if (wave == 0) mean[lane] = n > 0 ? ksum * (1.0f / (float)n) : 0.f;  // Scale(mean, 1/n)
+    __syncthreads();
+    // centred rows quantised per key (quantRowAVX2 without the flip,
+    // attention8.go:240-251); padding slots [n, npad) get zeros
+    int8_t *kp = a.kp + ((size_t)h * a.Npad + slot0) * D;
+    float *ks = a.ks + (size_t)h * a.Npad + slot0;
+    const float4 mu = *(const float4 *)&mean[4 * sub];
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      const int j = rg + 32 * u;
+      if (j < npad) {  // uniform over the 16 lanes of a row
+        int kq = 0;
+        float sc = 0.f;
+        if (j < n) {
+          const float4 c = make_float4(kr[u].x - mu.x, kr[u].y - mu.y, kr[u].z - mu.z, kr[u].w - mu.w);
+          float mx = fmax32(fmax32(fabsf(c.x), fabsf(c.y)), fmax32(fabsf(c.z), fabsf(c.w)));
+          for (int t = 1; t < 16; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t, 16));
+          float inv = 0.f;
+          if (mx != 0.f) {
+            sc = mx / 127.0f;
+            inv = 1.0f / sc;
+          }
+          kq = pack4(q8(c.x, inv), q8(c.y, inv), q8(c.z, inv), q8(c.w, inv));
+        }
+        *(int *)(kp + (size_t)j * D + 4 * sub) = kq;
+        if (sub == 0) ks[j] = sc;
+      }
+    }
+  } else {
+    float4 vr[16];
+    const uint32_t voff = (uint32_t)(16 * rg) * ld * 4 + col + 4 * H;
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      const int j = 16 * rg + u;
+      vr[u] = j < n ? buf_load_f4(rows, voff, (uint32_t)u * ld * 4) : zero4;
+    }
+    // max |V| per dimension (MaxAbsTo, attention8.go:259-261)
+    float4 vm = zero4;
+#pragma unroll
+    for (int u = 0; u < 16; u++)
+      vm = make_float4(fmax32(vm.x, fabsf(vr[u].x)), fmax32(vm.y, fabsf(vr[u].y)),
+                       fmax32(vm.z, fabsf(vr[u].z)), fmax32(vm.w, fabsf(vr[u].w)));
+    for (int t = 16; t < 64; t <<= 1) {
+      vm.x = fmax32(vm.x, __shfl_xor(vm.x, t));
+      vm.y = fmax32(vm.y, __shfl_xor(vm.y, t));
+      vm.z = fmax32(vm.z, __shfl_xor(vm.z, t));
+      vm.w = fmax32(vm.w, __shfl_xor(vm.w, t));
+    }
+    if (lane < 16) *(float4 *)&red[wave][4 * sub] = vm;
+    __syncthreads();
+    if (tid < D) {
+      float vs = 0.f;
+      for (int g = 0; g < 8; g++) vs = fmax32(vs, red[g][tid]);
+      float vi = 0.f;
+      if (vs > 0.f) {  // attention8.go:262-269
+        vs = vs / 127.0f;
+        vi = 1.0f / vs;
+      }
+      mean[tid] = vi;
+      a.vs[((size_t)b * a.nh + h) * D + tid] = vs;
+    }
+    __syncthreads();
+    // quantCols (attention8.go:270-279), 16 keys of a dimension per store
+    const float4 vi = *(const float4 *)&mean[4 * sub];
+    if (16 * rg < npad) {
+      int8_t *vt = a.vt + ((size_t)h * D + 4 * sub) * a.Npad + slot0 + 16 * rg;
+      int w[4][4];
+#pragma unroll
+      for (int u = 0; u < 16; u += 4) {
+        w[0][u / 4] = pack4(q8(vr[u].x, vi.x), q8(vr[u + 1].x, vi.x), q8(vr[u + 2].x, vi.x), q8(vr[u + 3].x, vi.x));
+        w[1][u / 4] = pack4(q8(vr[u].y, vi.y), q8(vr[u + 1].y, vi.y), q8(vr[u + 2].y, vi.y), q8(vr[u + 3].y, vi.y));
+        w[2][u / 4] = pack4(q8(vr[u].z, vi.z), q8(vr[u + 1].z, vi.z), q8(vr[u + 2].z, vi.z), q8(vr[u + 3].z, vi.z));
+        w[3][u / 4] = pack4(q8(vr[u].w, vi.w), q8(vr[u + 1].w, vi.w), q8(vr[u + 2].w, vi.w), q8(vr[u + 3].w, vi.w));
+      }
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const v4i o = {w[c][0], w[c][1], w[c][2], w[c][3]};
+        *(v4i *)(vt + (size_t)c * a.Npad) = o;
+      }
+    }
   }
 }
 
@@ -461,8 +600,11 @@ void launch_attn_quant_q(const AttnArgs &a, hipStream_t s) {
 
 void launch_attn_prologue(const AttnArgs &a, hipStream_t s) {
   if (a.B <= 0) return;
-  dim3 grid(a.B, a.nh);
-  attn_prologue_kernel<<<grid, 256, 0, s>>>(a);
+  if (a.max_n <= kShortSeq) {
+    attn_prologue_short_kernel<<<dim3(a.B, a.nh, 2), 512, 0, s>>>(a);
+  } else {
+    attn_prologue_kernel<<<dim3(a.B, a.nh), 256, 0, s>>>(a);
+  }
 }
 
 void launch_attn_main(const AttnArgs &a, hipStream_t s) {

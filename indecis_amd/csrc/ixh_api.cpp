@@ -556,6 +556,8 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   aa.offs = w->offs.as<int32_t>();
   aa.padoff = w->padoff.as<int32_t>();
   aa.B = B;
+  aa.max_n = 0;
+  for (int b = 0; b < B; b++) aa.max_n = std::max(aa.max_n, offs[b + 1] - offs[b]);
   aa.scale = (float)(1.0 / std::sqrt((double)D));  // infer.go:445
   aa.lanes = c.lanes;
   aa.qq = w->qq.as<int8_t>();
@@ -1232,6 +1234,7 @@ int ixh_attend8(int device, float *o, const float *q, const float *k, const floa
   aa.offs = dtabs.as<int32_t>();
   aa.padoff = dtabs.as<int32_t>() + 2;
   aa.B = 1;
+  aa.max_n = n;
   aa.scale = scale;
   aa.window = window;
   aa.lanes = lanes;

@@ -69,6 +69,17 @@ __device__ __forceinline__ float exp32_simd(float v) {
   return under ? 0.0f : y * pw;
 }
 
+// Buffer resource over `bytes` bytes from p (gfx9 descriptor word 3), for
+// loads that share one VGPR offset and step by a wave-uniform SGPR offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float4 buf_load_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const v4i t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_float4(__int_as_float(t[0]), __int_as_float(t[1]), __int_as_float(t[2]),
+                     __int_as_float(t[3]));
+}
+
 // 255*exp(v) from the hardware base-2 exponential (v_exp_f32): fma(v,
 // log2 e, log2 255), then 2^x. Used only to round: where it lies more than
 // kExp255Tol from a half-integer, RNE of it equals RNE(f32(255*exp32(v)))

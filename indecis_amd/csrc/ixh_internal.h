@@ -97,6 +97,7 @@ struct AttnArgs {
   const int32_t *offs;     // [B+1]
   const int32_t *padoff;   // [B+1] start of each sequence's key slots
   int B;
+  int max_n;               // longest sequence (picks the prologue variant)
   float scale;             // 1/sqrt(D)
   int window;              // <0 global
   int lanes;

@@ -174,3 +174,18 @@ def test_invalidate_requires_upload():
     m.upload(w)
     assert f32_bits_equal(m.encode_seqs(seq), before)
     m.close()
+
+
+@pytest.mark.parametrize("longest", [512, 513])
+def test_prologue_edge_lengths(longest):
+    """Sequence lengths around the attention prologue's 32-key pieces and
+    64-slot padding, with the longest at 512 (single-read prologue) or 513
+    (the two-pass prologue for longer sequences)."""
+    cfg = small_cfg()
+    w, gpu, ora = model_pair(cfg, seed=11)
+    rng = np.random.default_rng(longest)
+    seqs = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32)
+            for n in (1, 31, 32, 33, 64, 65, 127, longest, 0, 2)]
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
