@@ -234,87 +234,150 @@ __global__ __launch_bounds__(64) void rownorm_lds_kernel(RowArgs a) {
   __shared__ __attribute__((aligned(16))) float xs[RPW * LD];
   __shared__ float rmean[RPW], rrstd[RPW];
   const int lane = threadIdx.x;
-  const int row0 = blockIdx.x * RPW;
+  const int groups = (a.M + RPW - 1) / RPW;
+  // The grid holds at most as many waves as fit on the device at once; each
+  // wave walks row groups blockIdx.x, + gridDim.x, ... and loads the next
+  // group into registers while the current one runs from LDS.
   float4 x[RPW][CPL];
+  auto load = [&](int grp) {
 #pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    const int R = min(row0 + r, a.M - 1);  // rows past M repeat the last one
-    const RowLoad<SRC> src(a, R);
+    for (int r = 0; r < RPW; r++) {
+      const int R = min(grp * RPW + r, a.M - 1);  // rows past M repeat the last one
+      const RowLoad<SRC> src(a, R);
 #pragma unroll
-    for (int c = 0; c < CPL; c++) x[r][c] = src.load4(4 * (lane + 64 * c));
-  }
-#pragma unroll
-  for (int r = 0; r < RPW; r++)
-#pragma unroll
-    for (int c = 0; c < CPL; c++) *(float4 *)&xs[r * LD + 4 * (lane + 64 * c)] = x[r][c];
+      for (int c = 0; c < CPL; c++) x[r][c] = src.load4(4 * (lane + 64 * c));
+    }
+  };
   const bool ln = a.gamma != nullptr;
-  if (ln) {
-    __syncthreads();
-    const int r = lane / V, l = lane % V;
-    const float *xr = &xs[r * LD + l];
-    float p = 0.f;
-#pragma unroll
-    for (int k = 0; k < H / V; k++) p = p + xr[V * k];
-    double sum = 0.0;  // lanes in order, in float64 (vec_simd.go:294-297)
-#pragma unroll
-    for (int t = 0; t < V; t++) sum += (double)__shfl(p, r * V + t);
-    const float mean = (float)(sum / (double)H);
-    float q = 0.f;
-#pragma unroll
-    for (int k = 0; k < H / V; k++) {
-      const float d = xr[V * k] - mean;
-      q = __builtin_fmaf(d, d, q);
-    }
-    double var = 0.0;
-#pragma unroll
-    for (int t = 0; t < V; t++) var += (double)__shfl(q, r * V + t);
-    if (l == 0) {
-      rmean[r] = mean;
-      rrstd[r] = (float)(1.0 / __builtin_sqrt(var / (double)H + a.eps));
-    }
-    __syncthreads();
-  }
   float4 g[CPL];
   if (ln) {
 #pragma unroll
     for (int c = 0; c < CPL; c++) g[c] = *(const float4 *)&a.gamma[4 * (lane + 64 * c)];
   }
+  int grp = blockIdx.x;
+  load(grp);
+  for (; grp < groups; grp += gridDim.x) {
+    __syncthreads();  // the previous group's output pass is done with xs
 #pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    const int R = row0 + r;
-    if (R >= a.M) break;  // wave-uniform
-    float mx = 0.f;
+    for (int r = 0; r < RPW; r++)
 #pragma unroll
-    for (int c = 0; c < CPL; c++) {
-      float4 v = x[r][c];
-      if (ln) {
-        const float mean = rmean[r], rstd = rrstd[r];
-        v = make_float4(((v.x - mean) * rstd) * g[c].x, ((v.y - mean) * rstd) * g[c].y,
-                        ((v.z - mean) * rstd) * g[c].z, ((v.w - mean) * rstd) * g[c].w);
-        x[r][c] = v;
+      for (int c = 0; c < CPL; c++) *(float4 *)&xs[r * LD + 4 * (lane + 64 * c)] = x[r][c];
+    if (grp + (int)gridDim.x < groups) load(grp + gridDim.x);
+    __syncthreads();
+    if (ln) {
+      const int r = lane / V, l = lane % V;
+      const float *xr = &xs[r * LD + l];
+      float p = 0.f;
+#pragma unroll
+      for (int k = 0; k < H / V; k++) p = p + xr[V * k];
+      double sum = 0.0;  // lanes in order, in float64 (vec_simd.go:294-297)
+#pragma unroll
+      for (int t = 0; t < V; t++) sum += (double)__shfl(p, r * V + t);
+      const float mean = (float)(sum / (double)H);
+      float q = 0.f;
+#pragma unroll
+      for (int k = 0; k < H / V; k++) {
+        const float d = xr[V * k] - mean;
+        q = __builtin_fmaf(d, d, q);
       }
-      if (a.out) *(float4 *)(a.out + (size_t)R * H + 4 * (lane + 64 * c)) = v;
-      mx = fmax32(mx, fmax32(fmax32(fabsf(v.x), fabsf(v.y)), fmax32(fabsf(v.z), fabsf(v.w))));
+      double var = 0.0;
+#pragma unroll
+      for (int t = 0; t < V; t++) var += (double)__shfl(q, r * V + t);
+      if (l == 0) {
+        rmean[r] = mean;
+        rrstd[r] = (float)(1.0 / __builtin_sqrt(var / (double)H + a.eps));
+      }
+      __syncthreads();
+    }
+    // Output in three steps so the RPW wave reductions overlap: normalise
+    // every row (back into LDS when it is quantised next) with its max |o|,
+    // reduce the RPW maxima together, then quantise.
+    float mx[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      const int R = min(grp * RPW + r, a.M - 1);  // rows past M: computed, not stored
+      mx[r] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPL; c++) {
+        float4 *px = (float4 *)&xs[r * LD + 4 * (lane + 64 * c)];
+        float4 v = *px;
+        if (ln) {
+          const float mean = rmean[r], rstd = rrstd[r];
+          v = make_float4(((v.x - mean) * rstd) * g[c].x, ((v.y - mean) * rstd) * g[c].y,
+                          ((v.z - mean) * rstd) * g[c].z, ((v.w - mean) * rstd) * g[c].w);
+          if (a.q) *px = v;
+        }
+        if (a.out && grp * RPW + r < a.M) *(float4 *)(a.out + (size_t)R * H + 4 * (lane + 64 * c)) = v;
+        // |o| has no NaN and no -0, so max picks the same value as the
+        // reference's compare
+        mx[r] = __builtin_fmaxf(mx[r], __builtin_fmaxf(__builtin_fmaxf(fabsf(v.x), fabsf(v.y)),
+                                                       __builtin_fmaxf(fabsf(v.z), fabsf(v.w))));
+      }
     }
     if (!a.q) continue;
 #pragma unroll
-    for (int t = 1; t < 64; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t));
-    float s = 0.f, inv = 0.f;
-    if (mx != 0.f) {  // quantizeA (linalg/int8.go:160-191)
-      s = mx / 127.0f;
-      inv = 1.0f / s;
-    }
-    int8_t *qrow = a.q + (size_t)R * a.ldq;
+    for (int t = 1; t < 64; t <<= 1)
 #pragma unroll
-    for (int c = 0; c < CPL; c++) {
-      const float4 v = x[r][c];
-      const int q0 = q8(v.x, inv), q1 = q8(v.y, inv), q2 = q8(v.z, inv), q3 = q8(v.w, inv);
-      *(int *)(qrow + 4 * (lane + 64 * c)) =
-          (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+      for (int r = 0; r < RPW; r++) mx[r] = __builtin_fmaxf(mx[r], __shfl_xor(mx[r], t));
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      const int R = grp * RPW + r;
+      if (R >= a.M) break;  // wave-uniform
+      float s = 0.f, inv = 0.f;
+      if (mx[r] != 0.f) {  // quantizeA (linalg/int8.go:160-191)
+        s = mx[r] / 127.0f;
+        inv = 1.0f / s;
+      }
+      int8_t *qrow = a.q + (size_t)R * a.ldq;
+#pragma unroll
+      for (int c = 0; c < CPL; c++) {
+        const float4 v = *(const float4 *)&xs[r * LD + 4 * (lane + 64 * c)];
+        const int q0 = q8(v.x, inv), q1 = q8(v.y, inv), q2 = q8(v.z, inv), q3 = q8(v.w, inv);
+        *(int *)(qrow + 4 * (lane + 64 * c)) =
+            (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+      }
+      for (int i = H + lane; i < a.ldq; i += 64) qrow[i] = 0;
+      if (lane == 0) a.sa[R] = s;
     }
-    for (int i = H + lane; i < a.ldq; i += 64) qrow[i] = 0;
-    if (lane == 0) a.sa[R] = s;
   }
+}
+
+// quantizeA on f32 rows with the row in registers (CPL float4 per lane,
+// K <= 256*CPL): one wave per row, every load in flight before the max.
+template <int CPL>
+__global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float *x, int ld, int M, int K,
+                                                             int8_t *q, int ldq, float *sa) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= M) return;
+  const float *row = x + (size_t)r * ld;
+  float4 v[CPL];
+  float mx = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPL; c++) {
+    const int i = 4 * (lane + 64 * c);
+    v[c] = i < K ? *(const float4 *)(row + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int c = 0; c < CPL; c++)
+    mx = fmax32(mx, fmax32(fmax32(fabsf(v[c].x), fabsf(v[c].y)), fmax32(fabsf(v[c].z), fabsf(v[c].w))));
+  for (int t = 1; t < 64; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t));
+  float s = 0.f, inv = 0.f;
+  if (mx != 0.f) {
+    s = mx / 127.0f;
+    inv = 1.0f / s;
+  }
+  int8_t *qrow = q + (size_t)r * ldq;
+#pragma unroll
+  for (int c = 0; c < CPL; c++) {
+    const int i = 4 * (lane + 64 * c);
+    if (i < K) {
+      const int q0 = q8(v[c].x, inv), q1 = q8(v[c].y, inv), q2 = q8(v[c].z, inv), q3 = q8(v[c].w, inv);
+      *(int *)(qrow + i) = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+    }
+  }
+  for (int i = K + lane; i < ldq; i += 64) qrow[i] = 0;
+  if (lane == 0) sa[r] = s;
 }
 
 // One wave per row: quantizeA on rows of f32 (no LayerNorm).
@@ -388,6 +451,23 @@ __global__ void head_logits_kernel(const float *x, int T, int H, const float *w,
   z[g] = s + (double)b[r];
 }
 
+// Launches kern with min(work, the workgroups that fit on the device at
+// once) workgroups of `threads`; the kernel strides over the rest.
+template <typename Kern>
+void launch_resident(Kern kern, int work, int threads, const RowArgs &a, hipStream_t s) {
+  static int resident[64];  // per device; 0 until first asked
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  int &n = resident[dev & 63];
+  if (n == 0) {
+    int cus = 0, per_cu = 0;
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)kern, threads, 0);
+    n = std::max(1, cus * per_cu);
+  }
+  kern<<<std::min(work, n), threads, 0, s>>>(a);
+}
+
 }  // namespace
 
 void launch_rownorm(const RowArgs &a, hipStream_t s) {
@@ -395,14 +475,14 @@ void launch_rownorm(const RowArgs &a, hipStream_t s) {
   const int src = !a.ids ? 0 : a.emb_format == 0 ? 1 : a.emb_format == 1 ? 2 : 3;
   if (a.lanes > 0 && a.H % 256 == 0 && a.H <= 1024 && !(a.lanes == 4 && a.H > 768)) {
     const int V = a.lanes, cpl = a.H / 256, rpw = 64 / V;
-    const dim3 grid((a.M + rpw - 1) / rpw);
+    const int groups = (a.M + rpw - 1) / rpw;
 #define IXH_LN(VV, CC)                                                                   \
   if (V == VV && cpl == CC) {                                                            \
     switch (src) {                                                                       \
-    case 0: rownorm_lds_kernel<VV, CC, 0><<<grid, 64, 0, s>>>(a); return;               \
-    case 1: rownorm_lds_kernel<VV, CC, 1><<<grid, 64, 0, s>>>(a); return;               \
-    case 2: rownorm_lds_kernel<VV, CC, 2><<<grid, 64, 0, s>>>(a); return;               \
-    default: rownorm_lds_kernel<VV, CC, 3><<<grid, 64, 0, s>>>(a); return;              \
+    case 0: launch_resident(rownorm_lds_kernel<VV, CC, 0>, groups, 64, a, s); return;    \
+    case 1: launch_resident(rownorm_lds_kernel<VV, CC, 1>, groups, 64, a, s); return;    \
+    case 2: launch_resident(rownorm_lds_kernel<VV, CC, 2>, groups, 64, a, s); return;    \
+    default: launch_resident(rownorm_lds_kernel<VV, CC, 3>, groups, 64, a, s); return;   \
     }                                                                                    \
   }
     IXH_LN(4, 1) IXH_LN(4, 2) IXH_LN(4, 3)
@@ -423,7 +503,16 @@ void launch_rownorm(const RowArgs &a, hipStream_t s) {
 void launch_quant_rows(const float *x, int ld, int M, int K, int8_t *q, int ldq, float *sa,
                        hipStream_t s) {
   if (M <= 0) return;
-  quant_rows_kernel<<<(M + 3) / 4, 256, 0, s>>>(x, ld, M, K, q, ldq, sa);
+  const dim3 grid((M + 3) / 4);
+  switch ((K + 255) / 256) {
+  case 1: quant_rows_reg_kernel<1><<<grid, 256, 0, s>>>(x, ld, M, K, q, ldq, sa); break;
+  case 2: quant_rows_reg_kernel<2><<<grid, 256, 0, s>>>(x, ld, M, K, q, ldq, sa); break;
+  case 3: quant_rows_reg_kernel<3><<<grid, 256, 0, s>>>(x, ld, M, K, q, ldq, sa); break;
+  case 4: quant_rows_reg_kernel<4><<<grid, 256, 0, s>>>(x, ld, M, K, q, ldq, sa); break;
+  case 5: quant_rows_reg_kernel<5><<<grid, 256, 0, s>>>(x, ld, M, K, q, ldq, sa); break;
+  case 6: quant_rows_reg_kernel<6><<<grid, 256, 0, s>>>(x, ld, M, K, q, ldq, sa); break;
+  default: quant_rows_kernel<<<grid, 256, 0, s>>>(x, ld, M, K, q, ldq, sa); break;
+  }
 }
 
 void launch_positions(const int32_t *offs, const int32_t *padoff, int B, int32_t *pos,
