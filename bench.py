@@ -85,7 +85,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="cfg4", choices=sorted(WORKLOADS))
     ap.add_argument("--lanes", type=int, default=8)
-    ap.add_argument("--cpu-tokens", type=int, default=4096,
+    ap.add_argument("--cpu-tokens", type=int, default=24576,
                     help="tokens of the batch timed on the CPU baseline (0: skip)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one device copy of 512 MiB (PMC calibration)")
