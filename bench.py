@@ -10,10 +10,13 @@ weights of the ModernBERT-base shape (H 768, 22 layers, 12 heads, GeGLU
 pooled [256, 768] output stays there (ixh_encode_device).
 
 Prints one JSON line. `roofline` is for the kernel class with the most GPU
-time, from HIP events recorded around every launch during the timed steps
-(algorithmic int8 ops or HBM bytes per launch over the average launch
-duration); `traffic` comes from a committed rocprofv3 PMC summary of that
-kernel (profiles/pmc_<kernel>.json) when one matches, else null.
+time in one untimed pass whose launches are all timed by HIP events; during
+the K timed steps the library brackets that class's launches (only) with
+timing-only HIP events on its stream, and `achieved` is its algorithmic int8
+ops (or HBM bytes) per launch over their average duration. `traffic` comes
+from a committed rocprofv3 PMC summary of that kernel
+(profiles/pmc_<kernel>.json) when one matches, else null. `kernels` is the
+per-class breakdown of the untimed pass.
 `cpu_baseline` times the C restatement of the reference (oracle/, test
 infrastructure) on a bounded sample of the same batch on the host cores.
 """
@@ -129,7 +132,17 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    # One untimed pass with every launch bracketed by events: the per-class
+    # breakdown and the dominant class.
     model.set_profiling(True)
+    step()
+    torch.cuda.synchronize()
+    breakdown = model.profile()
+    dom = max(breakdown, key=lambda k: breakdown[k]["ms"])
+
+    # Timed region: events around the dominant class's launches only (two
+    # per launch, on the library's stream), wall clock around the K steps.
+    model.set_profiling(True, only=dom)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -140,26 +153,24 @@ def main():
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    prof = model.profile()
+    d = model.profile()[dom]
     model.set_profiling(False)
     gpu_ms = ev0.elapsed_time(ev1) / args.steps
     ms_per_step = wall * 1000 / args.steps
 
-    # per-class figures per step and the dominant class
+    # per-class figures of the untimed pass (one step)
     kernels = {}
-    for name, s in prof.items():
-        per_launch_ms = s["ms"] / max(s["launches"], 1)
-        if s["ops"] > 0:
-            ach = s["ops"] / (s["ms"] / 1e3) / 1e12
-            kernels[name] = {"ms_per_step": round(s["ms"] / args.steps, 3), "TOP/s": round(ach, 1),
+    for name, st in breakdown.items():
+        per_launch_ms = st["ms"] / max(st["launches"], 1)
+        if st["ops"] > 0:
+            ach = st["ops"] / (st["ms"] / 1e3) / 1e12
+            kernels[name] = {"ms_per_step": round(st["ms"], 3), "TOP/s": round(ach, 1),
                              "mfma_frac": round(ach * 1e12 / PEAK_INT8_OPS, 4)}
         else:
-            ach = s["bytes"] / (s["ms"] / 1e3) / 1e9
-            kernels[name] = {"ms_per_step": round(s["ms"] / args.steps, 3), "GB/s": round(ach, 1),
+            ach = st["bytes"] / (st["ms"] / 1e3) / 1e9
+            kernels[name] = {"ms_per_step": round(st["ms"], 3), "GB/s": round(ach, 1),
                              "hbm_frac": round(ach * 1e9 / PEAK_HBM, 4)}
         kernels[name]["avg_launch_us"] = round(per_launch_ms * 1e3, 2)
-    dom = max(prof, key=lambda k: prof[k]["ms"])
-    d = prof[dom]
     avg_s = d["ms"] / d["launches"] / 1e3
     if d["ops"] > 0:
         per_launch = d["ops"] / d["launches"]
@@ -174,9 +185,10 @@ def main():
     roof["kernel"] = dom
     roof["algorithmic_per_launch"] = per_launch
     roof["avg_launch_us"] = round(avg_s * 1e6, 2)
-    gemm = [s for n, s in prof.items() if n.startswith("gemm_")]
-    gemm_ops = sum(s["ops"] for s in gemm)
-    gemm_ms = sum(s["ms"] for s in gemm)
+    roof["launches_timed"] = d["launches"]
+    gemm = [st for n, st in breakdown.items() if n.startswith("gemm_")]
+    gemm_ops = sum(st["ops"] for st in gemm)
+    gemm_ms = sum(st["ms"] for st in gemm)
 
     cpu = None
     if args.cpu_tokens > 0:
@@ -206,6 +218,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "kernels_note": "per kernel class, from one untimed pass with every launch timed by HIP events",
     }
     print(json.dumps(line), flush=True)
     model.close()

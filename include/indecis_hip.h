@@ -138,6 +138,10 @@ typedef struct ixh_kernel_stat {
   double bytes;     /* summed algorithmic HBM bytes */
 } ixh_kernel_stat;
 int ixh_model_set_profiling(ixh_model *m, int on);
+/* Restricts the timing to launches of one kernel class (NULL or "": every
+ * launch), so that a timed run carries two events per launch of that class
+ * only. Clears the sums. */
+int ixh_model_set_profile_filter(ixh_model *m, const char *kernel_class);
 /* Copies up to cap class records into out; *n receives the number of
  * classes. */
 int ixh_model_profile(ixh_model *m, ixh_kernel_stat *out, int cap, int *n);

@@ -19,7 +19,8 @@ EXPORTS = [
     "ixh_model_invalidate", "ixh_encode_seqs", "ixh_encode_tokens", "ixh_encode_device",
     "ixh_head_logits", "ixh_packb8_create", "ixh_packb8_destroy", "ixh_matmul8",
     "ixh_matmul8_tile", "ixh_layernorm_quant", "ixh_ln_matmul8_geglu", "ixh_attend8",
-    "ixh_model_set_profiling", "ixh_model_profile", "ixh_check_exp255",
+    "ixh_model_set_profiling", "ixh_model_set_profile_filter", "ixh_model_profile",
+    "ixh_check_exp255",
 ]
 
 IXH_OK, IXH_EINVAL, IXH_ERANGE, IXH_ESTATE, IXH_EHIP, IXH_ENOMEM = range(6)
@@ -88,6 +89,7 @@ def lib():
         "ixh_ln_matmul8_geglu": [vp, vp, C.c_int, vp, C.c_double, C.c_int, vp, vp],
         "ixh_attend8": [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int],
         "ixh_model_set_profiling": [vp, C.c_int],
+        "ixh_model_set_profile_filter": [vp, C.c_char_p],
         "ixh_model_profile": [vp, C.POINTER(IxhKernelStat), C.c_int, C.POINTER(C.c_int)],
         "ixh_check_exp255": [C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_float),
                              C.POINTER(C.c_int64)],

@@ -245,6 +245,7 @@ struct ixh_model {
   std::atomic<bool> weights_valid{true};
   std::atomic<bool> profiling{false};
   std::mutex prof_mu;
+  std::string prof_only;  // profile only this kernel class (empty: all)
   std::vector<StatAcc> stats;
   ~ixh_model() {
     for (Workspace *w : pool) delete w;
@@ -368,6 +369,7 @@ struct Prof {
   Workspace *w;
   hipStream_t st;
   bool on;
+  std::string only;  // bracket only launches of this class (empty: all)
   struct Rec {
     const char *name;
     int idx;
@@ -377,11 +379,15 @@ struct Prof {
   int used = 0;
   int err = IXH_OK;
 
-  int begin() {
-    if (!on || err) return -1;
+  int begin(const char *name) {
+    if (!on || err || (!only.empty() && only != name)) return -1;
     if ((int)w->events.size() < 2 * (used + 1)) {
+      // timing-only events: no system-scope fence (cache writeback and
+      // invalidation) on record; they are read after the stream is
+      // synchronised
       hipEvent_t a, b;
-      if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
+      if (hipEventCreateWithFlags(&a, hipEventDisableSystemFence) != hipSuccess ||
+          hipEventCreateWithFlags(&b, hipEventDisableSystemFence) != hipSuccess) {
         err = fail(IXH_EHIP, "modernbert: hip: event creation failed");
         return -1;
       }
@@ -477,9 +483,13 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     return rc;
 
   Prof prof{m, w, st, m->profiling.load()};
+  if (prof.on) {
+    std::lock_guard<std::mutex> lk(m->prof_mu);
+    prof.only = m->prof_only;
+  }
 #define RUN(name, ops, bytes, stmt)                                                      \
   do {                                                                                   \
-    const int pi_ = prof.begin();                                                        \
+    const int pi_ = prof.begin(name);                                                        \
     stmt;                                                                                \
     LAUNCHCK(name);                                                                      \
     prof.end(pi_, name, (double)(ops), (double)(bytes));                                 \
@@ -852,6 +862,14 @@ int ixh_model_set_profiling(ixh_model *m, int on) {
   std::lock_guard<std::mutex> lk(m->prof_mu);
   m->stats.clear();
   m->profiling.store(on != 0);
+  return IXH_OK;
+}
+
+int ixh_model_set_profile_filter(ixh_model *m, const char *kernel_class) {
+  if (!m) return fail(IXH_EINVAL, "modernbert: nil model");
+  std::lock_guard<std::mutex> lk(m->prof_mu);
+  m->stats.clear();
+  m->prof_only = kernel_class ? kernel_class : "";
   return IXH_OK;
 }
 

@@ -269,8 +269,10 @@ class Model:
                                              kind, C.c_void_p(out_ptr),
                                              C.c_void_p(stream) if stream else None))
 
-    def set_profiling(self, on):
-        """Per-kernel HIP-event timing of every encode (clears the sums)."""
+    def set_profiling(self, on, only=None):
+        """Per-kernel HIP-event timing of every encode (clears the sums);
+        `only` restricts it to one kernel class."""
+        _lib.check(self._L.ixh_model_set_profile_filter(self._h, (only or "").encode()))
         _lib.check(self._L.ixh_model_set_profiling(self._h, 1 if on else 0))
 
     def profile(self):
