@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -209,8 +210,11 @@ struct Workspace {
       pooled, flag;
   PinBuf host;
   std::vector<hipEvent_t> events;  // profiling: begin/end pairs, reused
+  hipEvent_t order[2] = {nullptr, nullptr};  // cross-stream ordering (no timing)
   ~Workspace() {
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
+    for (hipEvent_t e : order)
+      if (e) (void)hipEventDestroy(e);
     if (stream) (void)hipStreamDestroy(stream);
   }
 };
@@ -430,9 +434,26 @@ struct Prof {
   }
 };
 
-// The forward pass. ids/out are device pointers here.
+// Streams a large batch is split over: IXH_SPLIT=1 (one pass) .. 4; default 2
+// (read at every call: tuning and tests change it between calls).
+int split_parts() {
+  const char *e = getenv("IXH_SPLIT");
+  const int v = e ? atoi(e) : 2;
+  return v < 1 ? 1 : v > 4 ? 4 : v;
+}
+
+// What a forward pass issued but has not waited for: its profiling records
+// and the RoPE tables its kernels read.
+struct Pending {
+  std::unique_ptr<Prof> prof;
+  std::vector<std::shared_ptr<DevBuf>> hold;
+};
+
+// The forward pass. ids/out are device pointers here. With `defer` the
+// launches are only issued: the caller synchronises the stream, then calls
+// defer->prof->flush().
 int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
-            const int32_t *offs, int B, int out_kind, float *d_out) {
+            const int32_t *offs, int B, int out_kind, float *d_out, Pending *defer = nullptr) {
   const ixh_config &c = m->cfg;
   const int H = c.hidden, I = c.intermediate, nh = c.heads, D = m->D;
   const int N = offs[B];
@@ -477,12 +498,15 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   if (!blocks.empty())
     HIPCK(hipMemcpyAsync(w->blocks.p, hs + 2 * (B + 1), 4 * blocks.size(), hipMemcpyHostToDevice, st));
 
-  std::vector<std::shared_ptr<DevBuf>> hold;
+  Pending local;
+  Pending &pend = defer ? *defer : local;
+  std::vector<std::shared_ptr<DevBuf>> &hold = pend.hold;
   const float *rc_g, *rs_g, *rc_l, *rs_l;
   if ((rc = rope_for(m, 1, T, &rc_g, &rs_g, hold)) || (rc = rope_for(m, 0, T, &rc_l, &rs_l, hold)))
     return rc;
 
-  Prof prof{m, w, st, m->profiling.load()};
+  pend.prof.reset(new Prof{m, w, st, m->profiling.load()});
+  Prof &prof = *pend.prof;
   if (prof.on) {
     std::lock_guard<std::mutex> lk(m->prof_mu);
     prof.only = m->prof_only;
@@ -651,10 +675,89 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     RUN("pool", 0, dN * 4 * dH + (double)B * 4 * dH,
         launch_pool(w->xn.as<float>(), w->offs.as<int32_t>(), B, H, c.pooling == IXH_POOL_CLS, d_out, st));
 #undef RUN
+  if (defer) return prof.err;
   // tables used by queued work stay alive until the stream has run them
   HIPCK(hipStreamSynchronize(st));
   return prof.flush();
 }
+
+// Token count from which a batch is split over several streams.
+constexpr int kSplitTokens = 4096;
+
+// The batch as P parts of about equal token counts, each on its own stream
+// (the caller's, then those of extra workspaces), issued back to back: the
+// kernels of one part (say its GEMMs) share the CUs with those of another
+// (its attention or row kernels), which are bound by other resources.
+// Sequences are independent, so the results equal one pass's. Without
+// extra workspaces (or for a small batch): one pass.
+int forward_split(ixh_model *m, Workspace *w, Workspace *const *extra, int nextra, hipStream_t st,
+                  const int32_t *d_ids, const int32_t *offs, int B, int out_kind, float *d_out) {
+  const int N = offs[B];
+  const int P = std::min(nextra + 1, B);
+  if (P < 2 || N < kSplitTokens) return forward(m, w, st, d_ids, offs, B, out_kind, d_out);
+  // part p covers sequences [cut[p], cut[p+1]): the first starting at or
+  // past p*N/P
+  std::vector<int> cut(P + 1, B);
+  cut[0] = 0;
+  for (int p = 1; p < P; p++) {
+    int b = cut[p - 1];
+    while (b < B && (int64_t)P * offs[b] < (int64_t)p * N) b++;
+    cut[p] = std::max(b, cut[p - 1]);
+  }
+  const int H = m->cfg.hidden;
+  for (int k = 0; k < nextra; k++)
+    for (int e = 0; e < 2; e++)
+      if (!extra[k]->order[e]) HIPCK(hipEventCreateWithFlags(&extra[k]->order[e], hipEventDisableTiming));
+  // every part follows the work queued on st so far (not the other parts;
+  // delaying a part by some of the previous part's kernels gains nothing,
+  // the parts drift apart by themselves)
+  for (int p = 1; p < P; p++) {
+    HIPCK(hipEventRecord(extra[p - 1]->order[0], st));
+    HIPCK(hipStreamWaitEvent(extra[p - 1]->stream, extra[p - 1]->order[0], 0));
+  }
+  std::vector<Pending> pend(P);
+  std::vector<std::vector<int32_t>> offp(P);
+  int rc = IXH_OK;
+  for (int p = 0; p < P; p++) {
+    const int b0 = cut[p], b1 = cut[p + 1];
+    if (b1 <= b0) continue;
+    Workspace *wp = p == 0 ? w : extra[p - 1];
+    hipStream_t sp = p == 0 ? st : wp->stream;
+    offp[p].resize(b1 - b0 + 1);
+    for (int b = b0; b <= b1; b++) offp[p][b - b0] = offs[b] - offs[b0];
+    const size_t out_off = out_kind == IXH_OUT_POOLED ? (size_t)b0 * H : (size_t)offs[b0] * H;
+    const int r = forward(m, wp, sp, d_ids + offs[b0], offp[p].data(), b1 - b0, out_kind,
+                          d_out + out_off, &pend[p]);
+    if (r && !rc) rc = r;
+  }
+  // st waits for every part whatever happened, so nothing is left queued
+  for (int p = 1; p < P; p++) {
+    HIPCK(hipEventRecord(extra[p - 1]->order[1], extra[p - 1]->stream));
+    HIPCK(hipStreamWaitEvent(st, extra[p - 1]->order[1], 0));
+  }
+  HIPCK(hipStreamSynchronize(st));
+  if (rc) return rc;
+  for (int p = 0; p < P; p++)
+    if (pend[p].prof && (rc = pend[p].prof->flush())) return rc;
+  return IXH_OK;
+}
+
+// Extra workspaces for a split pass, returned to the pool on scope exit.
+struct ExtraWs {
+  ixh_model *m;
+  std::vector<Workspace *> ws;
+  ExtraWs(ixh_model *model, int N) : m(model) {
+    const int want = N >= kSplitTokens ? split_parts() - 1 : 0;
+    for (int k = 0; k < want; k++) {
+      Workspace *w = acquire(m);
+      if (!w) break;  // fewer parts
+      ws.push_back(w);
+    }
+  }
+  ~ExtraWs() {
+    for (Workspace *w : ws) release(m, w);
+  }
+};
 
 int check_offs(const int32_t *offs, int B) {
   if (B < 0 || (B > 0 && !offs)) return fail(IXH_EINVAL, "modernbert: inconsistent batch");
@@ -682,11 +785,14 @@ int encode_host(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, in
   WsGuard wg{m, acquire(m)};
   Workspace *w = wg.w;
   if (!w) return fail(IXH_EHIP, "modernbert: hip: stream creation failed");
+  ExtraWs ex(m, N);
   hipStream_t st = w->stream;
   const size_t out_elems = kind == IXH_OUT_TOKENS ? (size_t)N * H : (size_t)B * H;
   if ((rc = w->ids.ensure(4 * (size_t)N)) || (rc = w->pooled.ensure(4 * out_elems))) return rc;
   HIPCK(hipMemcpyAsync(w->ids.p, ids, 4 * (size_t)N, hipMemcpyHostToDevice, st));
-  if ((rc = forward(m, w, st, w->ids.as<int32_t>(), offs, B, kind, w->pooled.as<float>()))) return rc;
+  if ((rc = forward_split(m, w, ex.ws.data(), (int)ex.ws.size(), st, w->ids.as<int32_t>(), offs, B,
+                          kind, w->pooled.as<float>())))
+    return rc;
   HIPCK(hipMemcpyAsync(out, w->pooled.p, 4 * out_elems, hipMemcpyDeviceToHost, st));
   HIPCK(hipStreamSynchronize(st));
   return IXH_OK;
@@ -929,7 +1035,8 @@ int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs, i
     HIPCK(hipMemcpy(&id, d_ids + bad, 4, hipMemcpyDeviceToHost));
     return fail(IXH_ERANGE, "modernbert: id %d out of vocabulary", id);
   }
-  return forward(m, w, st, d_ids, offs, B, out_kind, d_out);
+  ExtraWs ex(m, N);
+  return forward_split(m, w, ex.ws.data(), (int)ex.ws.size(), st, d_ids, offs, B, out_kind, d_out);
 }
 
 int ixh_head_logits(ixh_model *m, const float *x, int T, const float *w, const float *b,

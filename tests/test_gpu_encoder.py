@@ -189,3 +189,21 @@ def test_prologue_edge_lengths(longest):
     got = gpu.encode_tokens(seqs)
     want, _ = ora.encode_tokens(seqs)
     assert f32_bits_equal(got, want), mismatch_report(got, want)
+
+
+@pytest.mark.parametrize("parts", ["2", "3"])
+def test_split_streams_exact(parts, monkeypatch):
+    """A batch of at least 4,096 tokens runs as parts on as many streams
+    (forward_split; IXH_SPLIT parts, default 2); token states and pooled
+    output equal the oracle's."""
+    monkeypatch.setenv("IXH_SPLIT", parts)
+    cfg = small_cfg(layers=3)
+    w, gpu, ora = model_pair(cfg, seed=21)
+    rng = np.random.default_rng(21)
+    seqs = ids_uniform_lengths(rng, 40, 64, 256, cfg.vocab)
+    assert sum(len(s) for s in seqs) >= 4096
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+    pooled = gpu.encode_seqs(seqs)
+    assert f32_bits_equal(pooled, ora.encode_seqs(seqs))
