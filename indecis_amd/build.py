@@ -22,9 +22,15 @@ FLAGS = [
 ]
 
 
+# Per-source flags. attention_i8.hip: MFMA results in VGPRs, so the score
+# tiles feed the VALU softmax without v_accvgpr_read moves (same register
+# total, same occupancy).
+EXTRA = {"attention_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src, verbose):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

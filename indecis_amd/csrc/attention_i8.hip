@@ -471,18 +471,21 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
       const int k0 = t * 32;
       const bool full = k0 >= cs_hi && k0 + 32 <= ce_lo;  // every key valid for every query
       float p[16];
-      unsigned undecided = 0;
+      // largest distance of 255 e from its rounding: one max per score,
+      // one compare per tile; the rare lanes past the tolerance recheck
+      // their scores one by one
+      float dev = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         sv[r] = sv[r] * sqv - m;  // s - max, as the reference forms it
         const float y = exp255_fast(sv[r]);
         p[r] = rne(y);
-        undecided |= (fabsf(y - p[r]) > 0.5f - kExp255Tol) ? 1u << r : 0u;
+        dev = __builtin_fmaxf(dev, fabsf(y - p[r]));  // no NaN here: one v_max
       }
-      if (undecided) {
+      if (dev > 0.5f - kExp255Tol) {
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          if (undecided & (1u << r)) {
+          if (fabsf(exp255_fast(sv[r]) - p[r]) > 0.5f - kExp255Tol) {
             const int j = k0 + acc_row(r, lane);
             const float e = (j >= ts) ? exp32_scalar(sv[r]) : exp32_simd(sv[r]);
             // QuantizeRowU8 (vec_simd.go:64-91): RNE(e*255) in [0, 255]
