@@ -16,8 +16,9 @@
 // the reference's two-pass one, exactly: pass 1 the row max of the valid
 // scores, pass 2 e = exp(s - max) (the vector formula, or exp32 on the
 // last len%V keys of a row as ExpShift does), P = RNE(255 e) as uint8,
-// normalised by 1/f32(sum P). P (0..255) does not fit int8: it is split
-// as 128*(P>>7) + (P&127), two exact MFMAs. Scores need
+// normalised by 1/f32(sum P). P (0..255) does not fit int8: the MFMA
+// takes P - 128 and the accumulators get 128 * (sum of V over the keys of
+// the tiles) added from per-chunk prefix sums, exactly. Scores need
 // ((f32(tile) - kzc)*ks)*sq with the uint8 tile; tile - kzc is exactly the
 // signed sum, so the kernel uses f32(sum q*k).
 #include "ixh_device.h"
@@ -307,10 +308,13 @@ __global__ __launch_bounds__(256) void attn_quant_q_kernel(AttnArgs a) {
 }
 
 template <bool GLOBAL>
-__global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t Ks[CHUNK * KS];
   __shared__ __attribute__((aligned(16))) int8_t Vs[D * VS];
   __shared__ __attribute__((aligned(16))) float kss[CHUNK];
+  // per 32-key group g of the staged chunk: vpre[g][d] = sum of V over the
+  // keys of groups 0..g (int, exact); 40 KB of LDS in all, 4 workgroups per CU
+  __shared__ __attribute__((aligned(16))) int vpre[CHUNK / 32][D];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = a.blocks[2 * blockIdx.x], Q0 = a.blocks[2 * blockIdx.x + 1];
@@ -395,7 +399,23 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
       v4i o0 = {w[0], w[2], w[4], w[6]}, o1 = {w[1], w[3], w[5], w[7]};
       *(v4i *)&Vs[d * VS + 32 * g] = o0;
       *(v4i *)&Vs[d * VS + 32 * g + 16] = o1;
+      int sum = 0;
+#pragma unroll
+      for (int u = 0; u < 8; u++) sum = __builtin_amdgcn_sdot4(w[u], 0x01010101, sum, false);
+      vpre[g][d] = sum;
     }
+  };
+  // after the barrier that follows stage_v: group sums -> prefix sums
+  auto prefix_v = [&] {
+    if (tid < D) {
+      int acc = 0;
+#pragma unroll
+      for (int g = 0; g < CHUNK / 32; g++) {
+        acc += vpre[g][tid];
+        vpre[g][tid] = acc;
+      }
+    }
+    __syncthreads();
   };
   // Scores of tile t without the query scale: f32(sum q*k) * ks, in the S^T
   // layout (rows = keys 8*(r/4) + 4*(lane/32) + r%4 of the tile, column =
@@ -427,6 +447,7 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
     stage_k(c0);
     if (one_chunk) stage_v(c0);
     __syncthreads();
+    if (one_chunk) prefix_v();
     const int t0 = max(wt0, c0 / 32), t1 = min(wt1, (c0 + CHUNK) / 32);
     for (int t = t0; t < t1; t++) {
       float sv[16];
@@ -447,15 +468,19 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
   m = fmax32(m, __shfl_xor(m, 32)) * sqv;
 
   // ---- pass 2: P = RNE(255 exp(s - m)), O^T += V^T . P^T ----
+  // P (0..255) enters the MFMA as P - 128 (an int8: the byte P ^ 0x80);
+  // the missing 128 * sum_j v[j][d] over every key of the tiles a wave
+  // processes is the same for all its queries and is added to the
+  // accumulators per chunk from the prefix sums: O stays exact.
   // P is rounded from the hardware exponential (exp255_fast) unless that
   // lands within kExp255Tol of a half-integer; there (about 1 score in 500)
   // the reference formula decides: exp32 on the tail keys j >= ts (all keys
   // when lanes = 0), ExpShift's vector formula elsewhere.
-  v16i ohi[2], olo[2];
+  v16i o[2];
 #pragma unroll
   for (int dt = 0; dt < 2; dt++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) ohi[dt][r] = olo[dt][r] = 0;
+    for (int r = 0; r < 16; r++) o[dt][r] = 0;
   unsigned psum = 0;
   for (int c0 = bk0; c0 < bk1; c0 += CHUNK) {
     if (!one_chunk) {
@@ -463,8 +488,24 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
       stage_k(c0);
       stage_v(c0);
       __syncthreads();
+      prefix_v();
     }
     const int t0 = max(wt0, c0 / 32), t1 = min(wt1, (c0 + CHUNK) / 32);
+    if (t1 > t0) {
+      // rows of this lane: dims dt*32 + 8g + 4*(lane/32) + 0..3
+#pragma unroll
+      for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int d0 = dt * 32 + 8 * g + 4 * (lane >> 5);
+          const int4 hi = *(const int4 *)&vpre[t1 - 1 - c0 / 32][d0];
+          const int4 lo = t0 > c0 / 32 ? *(const int4 *)&vpre[t0 - 1 - c0 / 32][d0] : int4{0, 0, 0, 0};
+          o[dt][4 * g] += 128 * (hi.x - lo.x);
+          o[dt][4 * g + 1] += 128 * (hi.y - lo.y);
+          o[dt][4 * g + 2] += 128 * (hi.z - lo.z);
+          o[dt][4 * g + 3] += 128 * (hi.w - lo.w);
+        }
+    }
     for (int t = t0; t < t1; t++) {
       float sv[16];
       scores(t, c0, sv);
@@ -509,16 +550,13 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
         pw[g] = w;
         psum = __builtin_amdgcn_udot4(w, 0x01010101u, psum, false);
       }
-      // P = 128*(P>>7) + (P&127): both halves fit int8
-      const v4i bh = {(int)((pw[0] >> 7) & 0x01010101u), (int)((pw[1] >> 7) & 0x01010101u),
-                      (int)((pw[2] >> 7) & 0x01010101u), (int)((pw[3] >> 7) & 0x01010101u)};
-      const v4i bl = {(int)(pw[0] & 0x7f7f7f7fu), (int)(pw[1] & 0x7f7f7f7fu),
-                      (int)(pw[2] & 0x7f7f7f7fu), (int)(pw[3] & 0x7f7f7f7fu)};
+      // P - 128 as int8
+      const v4i bp = {(int)(pw[0] ^ 0x80808080u), (int)(pw[1] ^ 0x80808080u),
+                      (int)(pw[2] ^ 0x80808080u), (int)(pw[3] ^ 0x80808080u)};
 #pragma unroll
       for (int dt = 0; dt < 2; dt++) {
         const v4i fv = *(const v4i *)&Vs[(dt * 32 + (lane & 31)) * VS + (t * 32 - c0) + 16 * (lane >> 5)];
-        ohi[dt] = mfma32(fv, bh, ohi[dt]);
-        olo[dt] = mfma32(fv, bl, olo[dt]);
+        o[dt] = mfma32(fv, bp, o[dt]);
       }
     }
   }
@@ -534,14 +572,14 @@ __global__ __launch_bounds__(256) void attn_main_kernel(AttnArgs a) {
       const int d0 = dt * 32 + acc_row(4 * g, lane);
       const float4 v4 = *(const float4 *)&vsd[d0];
       const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-      float o[4];
+      float ov[4];
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int r = 4 * g + u;
-        const int tile = 128 * ohi[dt][r] + olo[dt][r];
-        o[u] = (((float)tile - 0.0f) * vv[u]) * sp;
+        const int tile = o[dt][r];
+        ov[u] = (((float)tile - 0.0f) * vv[u]) * sp;
       }
-      *(float4 *)(orow + d0) = make_float4(o[0], o[1], o[2], o[3]);
+      *(float4 *)(orow + d0) = make_float4(ov[0], ov[1], ov[2], ov[3]);
     }
   }
 }
