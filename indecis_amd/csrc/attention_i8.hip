@@ -420,13 +420,16 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   // Scores of tile t without the query scale: f32(sum q*k) * ks, in the S^T
   // layout (rows = keys 8*(r/4) + 4*(lane/32) + r%4 of the tile, column =
   // this query). The score is that times sq.
-  auto scores = [&](int t, int c0, float *sv) {
-    v16i acc;
-#pragma unroll
-    for (int r = 0; r < 16; r++) acc[r] = 0;
+  // The integer tile of tile t (two MFMAs), then its scaled scores.
+  // (Issuing tile t+1's MFMAs before tile t's VALU work was tried: no gain.)
+  auto score_acc = [&](int t, int c0) {
+    v16i acc = {};
     const int8_t *kr = &Ks[(t * 32 - c0 + (lane & 31)) * KS + 16 * (lane >> 5)];
     acc = mfma32(*(const v4i *)kr, qb[0], acc);
     acc = mfma32(*(const v4i *)(kr + 32), qb[1], acc);
+    return acc;
+  };
+  auto score_scale = [&](int t, int c0, const v16i &acc, float *sv) {
     const float *kt = &kss[t * 32 - c0 + 4 * (lane >> 5)];
 #pragma unroll
     for (int g = 0; g < 4; g++) {
@@ -451,11 +454,11 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
     const int t0 = max(wt0, c0 / 32), t1 = min(wt1, (c0 + CHUNK) / 32);
     for (int t = t0; t < t1; t++) {
       float sv[16];
-      scores(t, c0, sv);
+      score_scale(t, c0, score_acc(t, c0), sv);
       const int k0 = t * 32;
       if (k0 >= cs_hi && k0 + 32 <= ce_lo) {  // every key valid for every query
 #pragma unroll
-        for (int r = 0; r < 16; r++) m = fmax32(m, sv[r]);
+        for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, sv[r]);  // no NaN: v_max
       } else {
 #pragma unroll
         for (int r = 0; r < 16; r++) {
@@ -508,7 +511,7 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
     }
     for (int t = t0; t < t1; t++) {
       float sv[16];
-      scores(t, c0, sv);
+      score_scale(t, c0, score_acc(t, c0), sv);
       const int k0 = t * 32;
       const bool full = k0 >= cs_hi && k0 + 32 <= ce_lo;  // every key valid for every query
       float p[16];
