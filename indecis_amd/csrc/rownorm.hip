@@ -12,6 +12,7 @@
 #include "ixh_internal.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace ixh {
 
@@ -217,6 +218,118 @@ __global__ __launch_bounds__(256) void rownorm_kernel(RowArgs a) {
     for (int i = tail_begin; i < H; i++) qrow[i] = (int8_t)q8(out_at(i, src.load1(i)), inv);
     for (int i = H; i < a.ldq; i++) qrow[i] = 0;
     a.sa[r] = s;
+  }
+}
+
+// LayerNorm (+ quantisation) for lanes V in {8, 16} and H = 256*CPL with
+// each wave's RPW = 64/V rows held in registers (lane t: columns
+// 4*(t + 64c)) and only one 256-column segment of them in LDS at a time:
+// lane (r, l) = (t / V, t % V) runs the reference's lane partial l of row r
+// — x[l], x[l+V], ... added in order — segment after segment, carrying the
+// partial across segments (the same additions in the same order as over
+// the whole row). About 8 KB of LDS per wave instead of the whole rows, so
+// four times as many waves share a CU; the output and quantisation passes
+// run from the registers.
+template <int V, int CPL, int SRC>
+__global__ __launch_bounds__(64) void rownorm_seg_kernel(RowArgs a) {
+  constexpr int RPW = 64 / V, H = 256 * CPL, LD = 256 + V;
+  __shared__ __attribute__((aligned(16))) float xs[RPW * LD];
+  const int lane = threadIdx.x;
+  const int grp = blockIdx.x;
+  float4 x[RPW][CPL];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int R = min(grp * RPW + r, a.M - 1);  // rows past M repeat the last one
+    const RowLoad<SRC> src(a, R);
+#pragma unroll
+    for (int c = 0; c < CPL; c++) x[r][c] = src.load4(4 * (lane + 64 * c));
+  }
+  const bool ln = a.gamma != nullptr;
+  const int rr = lane / V, l = lane % V;  // this lane's chain: row rr, lane partial l
+  float mean = 0.f, rstd = 1.f;           // of row rr
+  if (ln) {
+    // sum: the chain over segment c continues from segment c-1
+    float p = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+#pragma unroll
+      for (int r = 0; r < RPW; r++) *(float4 *)&xs[r * LD + 4 * lane] = x[r][c];
+      __builtin_amdgcn_wave_barrier();
+      const float *xr = &xs[rr * LD + l];
+#pragma unroll
+      for (int k = 0; k < 256 / V; k++) p = p + xr[V * k];
+      __builtin_amdgcn_wave_barrier();
+    }
+    double sum = 0.0;  // lanes in order, in float64 (vec_simd.go:294-297)
+#pragma unroll
+    for (int t = 0; t < V; t++) sum += (double)__shfl(p, rr * V + t);
+    mean = (float)(sum / (double)H);
+    float q = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+#pragma unroll
+      for (int r = 0; r < RPW; r++) *(float4 *)&xs[r * LD + 4 * lane] = x[r][c];
+      __builtin_amdgcn_wave_barrier();
+      const float *xr = &xs[rr * LD + l];
+#pragma unroll
+      for (int k = 0; k < 256 / V; k++) {
+        const float d = xr[V * k] - mean;
+        q = __builtin_fmaf(d, d, q);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    double var = 0.0;
+#pragma unroll
+    for (int t = 0; t < V; t++) var += (double)__shfl(q, rr * V + t);
+    rstd = (float)(1.0 / __builtin_sqrt(var / (double)H + a.eps));
+  }
+  // output from the registers; every row's max |o| reduced together
+  float mx[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int R = min(grp * RPW + r, a.M - 1);
+    const float mu = __shfl(mean, r * V), rs = __shfl(rstd, r * V);
+    mx[r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+      float4 v = x[r][c];
+      if (ln) {
+        const float4 g = *(const float4 *)&a.gamma[4 * (lane + 64 * c)];
+        v = make_float4(((v.x - mu) * rs) * g.x, ((v.y - mu) * rs) * g.y, ((v.z - mu) * rs) * g.z,
+                        ((v.w - mu) * rs) * g.w);
+        x[r][c] = v;
+      }
+      if (a.out && grp * RPW + r < a.M) *(float4 *)(a.out + (size_t)R * H + 4 * (lane + 64 * c)) = v;
+      // |o| has no NaN and no -0, so max picks the same value as the
+      // reference's compare
+      mx[r] = __builtin_fmaxf(mx[r], __builtin_fmaxf(__builtin_fmaxf(fabsf(v.x), fabsf(v.y)),
+                                                     __builtin_fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+  }
+  if (!a.q) return;
+#pragma unroll
+  for (int t = 1; t < 64; t <<= 1)
+#pragma unroll
+    for (int r = 0; r < RPW; r++) mx[r] = __builtin_fmaxf(mx[r], __shfl_xor(mx[r], t));
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int R = grp * RPW + r;
+    if (R >= a.M) break;  // wave-uniform
+    float s = 0.f, inv = 0.f;
+    if (mx[r] != 0.f) {  // quantizeA (linalg/int8.go:160-191)
+      s = mx[r] / 127.0f;
+      inv = 1.0f / s;
+    }
+    int8_t *qrow = a.q + (size_t)R * a.ldq;
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+      const float4 v = x[r][c];
+      const int q0 = q8(v.x, inv), q1 = q8(v.y, inv), q2 = q8(v.z, inv), q3 = q8(v.w, inv);
+      *(int *)(qrow + 4 * (lane + 64 * c)) =
+          (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+    }
+    for (int i = H + lane; i < a.ldq; i += 64) qrow[i] = 0;
+    if (lane == 0) a.sa[R] = s;
   }
 }
 
@@ -485,6 +598,21 @@ void launch_rownorm(const RowArgs &a, hipStream_t s) {
     default: launch_resident(rownorm_lds_kernel<VV, CC, 3>, groups, 64, a, s); return;   \
     }                                                                                    \
   }
+    // lanes 8 and 16: one wave per row group, rows in registers (8 KB of LDS)
+#define IXH_SEG(VV, CC)                                                                  \
+  if (V == VV && cpl == CC && seg) {                                                     \
+    switch (src) {                                                                       \
+    case 0: rownorm_seg_kernel<VV, CC, 0><<<groups, 64, 0, s>>>(a); return;             \
+    case 1: rownorm_seg_kernel<VV, CC, 1><<<groups, 64, 0, s>>>(a); return;             \
+    case 2: rownorm_seg_kernel<VV, CC, 2><<<groups, 64, 0, s>>>(a); return;             \
+    default: rownorm_seg_kernel<VV, CC, 3><<<groups, 64, 0, s>>>(a); return;            \
+    }                                                                                    \
+  }
+    const char *se = getenv("IXH_LN_SEG");  // IXH_LN_SEG=0: the whole-row LDS kernel
+    const bool seg = !(se && se[0] == '0');
+    IXH_SEG(8, 1) IXH_SEG(8, 2) IXH_SEG(8, 3) IXH_SEG(8, 4)
+    IXH_SEG(16, 1) IXH_SEG(16, 2) IXH_SEG(16, 3) IXH_SEG(16, 4)
+#undef IXH_SEG
     IXH_LN(4, 1) IXH_LN(4, 2) IXH_LN(4, 3)
     IXH_LN(8, 1) IXH_LN(8, 2) IXH_LN(8, 3) IXH_LN(8, 4)
     IXH_LN(16, 1) IXH_LN(16, 2) IXH_LN(16, 3) IXH_LN(16, 4)
