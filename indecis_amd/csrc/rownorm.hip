@@ -546,8 +546,18 @@ __global__ void pool_kernel(const float *xn, const int32_t *offs, int H, int cls
     *dst = xn[(size_t)o * H + k];
     return;
   }
+  // the float64 sum in token order; rows are loaded 16 ahead of the adds
   double acc = 0.0;
-  for (int t = 0; t < n; t++) acc += (double)xn[(size_t)(o + t) * H + k];
+  const float *col = xn + (size_t)o * H + k;
+  int t = 0;
+  for (; t + 16 <= n; t += 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) v[u] = col[(size_t)(t + u) * H];
+#pragma unroll
+    for (int u = 0; u < 16; u++) acc += (double)v[u];
+  }
+  for (; t < n; t++) acc += (double)col[(size_t)t * H];
   *dst = (float)(acc / (double)n);
 }
 
