@@ -45,140 +45,145 @@ __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
   return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | (d << 24);
 }
 
-// K mean and V max per (sequence, head), then K and V quantised. Q was
-// quantised by the QKV GEMM epilogue. 16 threads own a row (a float4 of
-// the head's 64 values each); K goes through LDS 64 keys at a time so the
-// 64 sequential float32 chains of the mean read it from LDS.
-__global__ __launch_bounds__(256) void attn_prologue_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) float kst[64 * D];
-  __shared__ float vmaxp[16][D];
-  __shared__ __attribute__((aligned(16))) float mean[D];
-  __shared__ __attribute__((aligned(16))) float vinv[D];
-  __shared__ __attribute__((aligned(16))) int8_t vtile[D][64 + 16];
-  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-  const int sub = tid & 15, rg = tid >> 4;
+constexpr int kShortSeq = 512;   // keys one prologue workgroup holds in registers
+constexpr int kStatRows = 256;   // keys per LDS slab of the long-sequence K chains
+constexpr int kStatStride = kStatRows + 4;
+
+// Statistics of a long sequence (more than kShortSeq keys) for
+// Attn8.Prepare (attention8.go:224-230, 259-269), split 8 ways per
+// (sequence, head): blockIdx.z 0..3 run the float32 chains of the K mean
+// of 16 dimensions each, in key order (AddTo, then Scale by f32(1/n));
+// blockIdx.z 4..7 take max |V| of 16 dimensions (MaxAbsTo). 4 threads own
+// a key's 16 values (a float4 each), 64 keys per load. The K chains read
+// their slab transposed from LDS (one dimension's keys contiguous), double
+// buffered, while the next slab's loads are in flight. Writes the V scale
+// to a.vs and, per (sequence, head), the K mean and 1/V scale to a.kstat.
+__global__ __launch_bounds__(256) void attn_long_stats_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float kt[2][16][kStatStride];
+  const int b = blockIdx.x, h = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
+  const int q = tid & 3, r0 = tid >> 2;
+  const bool isk = z < 4;
+  const int dg = (z & 3) * 16;
   const int base = a.offs[b], n = a.offs[b + 1] - base;
-  const int slot0 = a.padoff[b];
-  const int npad = (n + kKeyPad - 1) / kKeyPad * kKeyPad;
-  const int H = a.H, ld = 3 * H;
-  const float *kcol = a.qkv + (size_t)base * ld + H + h * D + 4 * sub;
-  const float *vcol = kcol + H;
-
-  // pass 1: sum of K in key order (AddTo, attention8.go:224-228) and
-  // max |V| per dimension (MaxAbsTo, attention8.go:259-261)
-  float ksum = 0.f;
-  float4 vm = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int c0 = 0; c0 < n; c0 += 64) {
-    for (int rr = rg; rr < 64; rr += 16) {
-      const int j = c0 + rr;
-      if (j < n) {
-        *(float4 *)&kst[rr * D + 4 * sub] = *(const float4 *)(kcol + (size_t)j * ld);
-        const float4 v = *(const float4 *)(vcol + (size_t)j * ld);
-        vm = make_float4(fmax32(vm.x, fabsf(v.x)), fmax32(vm.y, fabsf(v.y)),
-                         fmax32(vm.z, fabsf(v.z)), fmax32(vm.w, fabsf(v.w)));
+  const int ld = 3 * a.H;
+  const float *seq = a.qkv + (size_t)base * ld;
+  const uint32_t voff = 4u * ((uint32_t)r0 * ld + (isk ? a.H : 2 * a.H) + h * D + dg + 4 * q);
+  float *stat = a.kstat + ((size_t)b * a.nh + h) * 2 * D;
+  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 reg[4];
+  // rows c0 .. c0+255 through a buffer descriptor of the slab's valid rows:
+  // keys past the sequence read as 0
+#define IXH_STAT_LOAD(c0)                                                                   \
+  {                                                                                         \
+    const __amdgpu_buffer_rsrc_t rs =                                                       \
+        buf_rsrc(seq + (size_t)(c0) * ld, (uint32_t)min(kStatRows, n - (c0)) * ld * 4);     \
+    _Pragma("unroll") for (int u = 0; u < 4; u++) reg[u] = buf_load_f4(rs, voff, 256u * u * ld); \
+  }
+  if (isk) {
+    float ksum = 0.f;
+    if (n > 0) IXH_STAT_LOAD(0)
+    for (int c0 = 0, buf = 0; c0 < n; c0 += kStatRows, buf ^= 1) {
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int r = r0 + 64 * u;
+        kt[buf][4 * q][r] = reg[u].x;
+        kt[buf][4 * q + 1][r] = reg[u].y;
+        kt[buf][4 * q + 2][r] = reg[u].z;
+        kt[buf][4 * q + 3][r] = reg[u].w;
       }
-    }
-    __syncthreads();
-    if (tid < D) {
-      const int cnt = min(64, n - c0);
-      for (int rr = 0; rr < cnt; rr++) ksum = ksum + kst[rr * D + tid];
-    }
-    __syncthreads();
-  }
-  vmaxp[rg][4 * sub] = vm.x;
-  vmaxp[rg][4 * sub + 1] = vm.y;
-  vmaxp[rg][4 * sub + 2] = vm.z;
-  vmaxp[rg][4 * sub + 3] = vm.w;
-  __syncthreads();
-  if (tid < D) {
-    mean[tid] = n > 0 ? ksum * (1.0f / (float)n) : 0.f;  // Scale(mean, 1/n)
-    float vs = 0.f;
-    for (int g = 0; g < 16; g++) vs = fmax32(vs, vmaxp[g][tid]);
-    float vi = 0.f;
-    if (vs > 0.f) {  // attention8.go:262-269
-      vs = vs / 127.0f;
-      vi = 1.0f / vs;
-    }
-    vinv[tid] = vi;
-    a.vs[((size_t)b * a.nh + h) * D + tid] = vs;
-  }
-  __syncthreads();
-
-  // pass 2: K centred and quantised per key (quantRowAVX2 without the
-  // flip, attention8.go:240-251), V per dimension (quantCols,
-  // attention8.go:270-279) and transposed through LDS
-  int8_t *kp = a.kp + ((size_t)h * a.Npad + slot0) * D;
-  float *ks = a.ks + (size_t)h * a.Npad + slot0;
-  int8_t *vt = a.vt + (size_t)h * D * a.Npad + slot0;
-  const float4 mu = *(const float4 *)&mean[4 * sub];
-  const float4 vi = *(const float4 *)&vinv[4 * sub];
-  for (int c0 = 0; c0 < npad; c0 += 64) {
-    for (int rr = rg; rr < 64; rr += 16) {
-      const int j = c0 + rr;
-      int kq = 0, v0 = 0, v1 = 0, v2 = 0, v3 = 0;
-      float s = 0.f;
-      if (j < n) {
-        const float4 k = *(const float4 *)(kcol + (size_t)j * ld);
-        const float4 c = make_float4(k.x - mu.x, k.y - mu.y, k.z - mu.z, k.w - mu.w);
-        float mx = fmax32(fmax32(fabsf(c.x), fabsf(c.y)), fmax32(fabsf(c.z), fabsf(c.w)));
-        for (int t = 1; t < 16; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t, 16));
-        float inv = 0.f;
-        if (mx != 0.f) {
-          s = mx / 127.0f;
-          inv = 1.0f / s;
+      __syncthreads();  // also orders the previous chain on this buffer
+      if (c0 + kStatRows < n) IXH_STAT_LOAD(c0 + kStatRows)
+      if (tid < 16) {
+        const float *row = &kt[buf][tid][0];
+        const int cnt = min(kStatRows, n - c0);
+        int r = 0;
+        for (; r + 4 <= cnt; r += 4) {
+          const float4 v = *(const float4 *)(row + r);
+          ksum = ksum + v.x;
+          ksum = ksum + v.y;
+          ksum = ksum + v.z;
+          ksum = ksum + v.w;
         }
-        kq = pack4(q8(c.x, inv), q8(c.y, inv), q8(c.z, inv), q8(c.w, inv));
-        const float4 v = *(const float4 *)(vcol + (size_t)j * ld);
-        v0 = q8(v.x, vi.x);
-        v1 = q8(v.y, vi.y);
-        v2 = q8(v.z, vi.z);
-        v3 = q8(v.w, vi.w);
+        for (; r < cnt; r++) ksum = ksum + row[r];
       }
-      *(int *)(kp + (size_t)j * D + 4 * sub) = kq;
-      if (sub == 0) ks[j] = s;
-      vtile[4 * sub][rr] = (int8_t)v0;
-      vtile[4 * sub + 1][rr] = (int8_t)v1;
-      vtile[4 * sub + 2][rr] = (int8_t)v2;
-      vtile[4 * sub + 3][rr] = (int8_t)v3;
     }
-    __syncthreads();
-    {
-      const int d = tid >> 2, seg = tid & 3;
-      *(v4i *)(vt + (size_t)d * a.Npad + c0 + 16 * seg) = *(const v4i *)&vtile[d][16 * seg];
+    if (tid < 16) stat[dg + tid] = n > 0 ? ksum * (1.0f / (float)n) : 0.f;
+  } else {
+    float4 vm = zero4;
+    if (n > 0) IXH_STAT_LOAD(0)
+    for (int c0 = 0; c0 < n; c0 += kStatRows) {
+      float4 cur[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) cur[u] = reg[u];
+      if (c0 + kStatRows < n) IXH_STAT_LOAD(c0 + kStatRows)
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        vm = make_float4(fmax32(vm.x, fabsf(cur[u].x)), fmax32(vm.y, fabsf(cur[u].y)),
+                         fmax32(vm.z, fabsf(cur[u].z)), fmax32(vm.w, fabsf(cur[u].w)));
     }
+    // threads with the same q hold the same 4 dimensions: xor over r0
+    for (int t = 4; t < 64; t <<= 1) {
+      vm.x = fmax32(vm.x, __shfl_xor(vm.x, t));
+      vm.y = fmax32(vm.y, __shfl_xor(vm.y, t));
+      vm.z = fmax32(vm.z, __shfl_xor(vm.z, t));
+      vm.w = fmax32(vm.w, __shfl_xor(vm.w, t));
+    }
+    float4 *red = (float4 *)&kt[0][0][0];  // [wave][q]
+    if ((tid & 63) < 4) red[(tid >> 6) * 4 + q] = vm;
     __syncthreads();
+    if (tid < 16) {
+      const float *rf = (const float *)red;
+      float vs = 0.f;
+      for (int w = 0; w < 4; w++) vs = fmax32(vs, rf[w * 16 + tid]);
+      float vi = 0.f;
+      if (vs > 0.f) {  // attention8.go:262-269
+        vs = vs / 127.0f;
+        vi = 1.0f / vs;
+      }
+      a.vs[((size_t)b * a.nh + h) * D + dg + tid] = vs;
+      stat[D + dg + tid] = vi;
+    }
   }
+#undef IXH_STAT_LOAD
 }
 
-// Single-read prologue for sequences of at most kShortSeq keys: one
-// workgroup of 512 threads per (sequence, head, K or V) holds the
-// sequence's 64-wide head slice in registers (16 float4 per thread), so K
-// and V are read from HBM once.
-//  K (blockIdx.z 0): row j = rg + 32u (rg = tid/16, u < 16). The 64
+// Single-read prologue: one workgroup of 512 threads per (sequence, head,
+// K or V) holds up to kShortSeq keys of the 64-wide head slice in
+// registers (16 float4 per thread), so K and V are read from HBM once.
+// PART: a long sequence's keys in parts of kShortSeq (blockIdx.z = 2 part
+// + K/V), with the K mean and 1/V scale from attn_long_stats_kernel;
+// otherwise (all sequences at most kShortSeq) the statistics are computed
+// here.
+//  K (blockIdx.z even): row j = rg + 32u (rg = tid/16, u < 16). The 64
 //    sequential float32 chains of the mean run in wave 0 over 32-row pieces
 //    written to a double-buffered LDS slab (one barrier per piece); then
 //    each row is centred and quantised from registers.
-//  V (blockIdx.z 1): row j = 16 rg + u, so a thread holds 16 consecutive
+//  V (blockIdx.z odd): row j = 16 rg + u, so a thread holds 16 consecutive
 //    keys of 4 dimensions: max |V| per dimension by a block reduction, then
 //    each dimension's 16 quantised keys leave as one 16-byte store into
 //    V^T.
-constexpr int kShortSeq = 512;
-__global__ __launch_bounds__(512, 4) void attn_prologue_short_kernel(AttnArgs a) {
+template <bool PART>
+__global__ __launch_bounds__(512, 4) void attn_prologue_rows_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float kst[2][32 * D];
   __shared__ __attribute__((aligned(16))) float red[8][D];
   __shared__ __attribute__((aligned(16))) float mean[D];
   const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const int sub = tid & 15, rg = tid >> 4, wave = tid >> 6, lane = tid & 63;
-  const int base = a.offs[b], n = a.offs[b + 1] - base;
-  const int slot0 = a.padoff[b];
-  const int npad = (n + kKeyPad - 1) / kKeyPad * kKeyPad;
+  const int j0 = PART ? (int)(blockIdx.z >> 1) * kShortSeq : 0;  // first key of the part
+  const int nseq = a.offs[b + 1] - a.offs[b];
+  const int npseq = (nseq + kKeyPad - 1) / kKeyPad * kKeyPad;
+  if (PART && j0 >= npseq) return;  // j0 < npseq implies j0 < nseq
+  const int base = a.offs[b] + j0, n = min(nseq - j0, kShortSeq);
+  const int slot0 = a.padoff[b] + j0;
+  const int npad = min(npseq - j0, kShortSeq);
   const int H = a.H, ld = 3 * H;
+  const float *stat = a.kstat + ((size_t)b * a.nh + h) * 2 * D;
   // the sequence's rows of qkv; a row is 4*ld bytes
   const __amdgpu_buffer_rsrc_t rows = buf_rsrc(a.qkv + (size_t)base * ld, (uint32_t)n * ld * 4);
   const uint32_t col = 4u * (H + h * D + 4 * sub);  // byte offset of this thread's K float4
   const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
 
-  if (blockIdx.z == 0) {
+  if ((blockIdx.z & 1) == 0) {
     float4 kr[16];
     const uint32_t voff = (uint32_t)rg * ld * 4 + col;
 #pragma unroll
@@ -190,7 +195,7 @@ __global__ __launch_bounds__(512, 4) void attn_prologue_short_kernel(AttnArgs a)
     float ksum = 0.f;
 #pragma unroll
     for (int u = 0; u < 16; u++) {
-      if (32 * u < n) {  // block-uniform
+      if (!PART && 32 * u < n) {  // block-uniform
         *(float4 *)&kst[u & 1][rg * D + 4 * sub] = kr[u];
         __syncthreads();
         if (wave == 0) {
@@ -205,7 +210,7 @@ __global__ __launch_bounds__(512, 4) void attn_prologue_short_kernel(AttnArgs a)
         }
       }
     }
-    if (wave == 0) mean[lane] = n > 0 ? ksum * (1.0f / (float)n) : 0.f;  // Scale(mean, 1/n)
+    if (wave == 0) mean[lane] = PART ? stat[lane] : n > 0 ? ksum * (1.0f / (float)n) : 0.f;  // Scale(mean, 1/n)
     __syncthreads();
     // centred rows quantised per key (quantRowAVX2 without the flip,
     // attention8.go:240-251); padding slots [n, npad) get zeros
@@ -241,30 +246,34 @@ __global__ __launch_bounds__(512, 4) void attn_prologue_short_kernel(AttnArgs a)
       const int j = 16 * rg + u;
       vr[u] = j < n ? buf_load_f4(rows, voff, (uint32_t)u * ld * 4) : zero4;
     }
-    // max |V| per dimension (MaxAbsTo, attention8.go:259-261)
-    float4 vm = zero4;
+    if (PART) {
+      if (tid < D) mean[tid] = stat[D + tid];
+    } else {
+      // max |V| per dimension (MaxAbsTo, attention8.go:259-261)
+      float4 vm = zero4;
 #pragma unroll
-    for (int u = 0; u < 16; u++)
-      vm = make_float4(fmax32(vm.x, fabsf(vr[u].x)), fmax32(vm.y, fabsf(vr[u].y)),
-                       fmax32(vm.z, fabsf(vr[u].z)), fmax32(vm.w, fabsf(vr[u].w)));
-    for (int t = 16; t < 64; t <<= 1) {
-      vm.x = fmax32(vm.x, __shfl_xor(vm.x, t));
-      vm.y = fmax32(vm.y, __shfl_xor(vm.y, t));
-      vm.z = fmax32(vm.z, __shfl_xor(vm.z, t));
-      vm.w = fmax32(vm.w, __shfl_xor(vm.w, t));
-    }
-    if (lane < 16) *(float4 *)&red[wave][4 * sub] = vm;
-    __syncthreads();
-    if (tid < D) {
-      float vs = 0.f;
-      for (int g = 0; g < 8; g++) vs = fmax32(vs, red[g][tid]);
-      float vi = 0.f;
-      if (vs > 0.f) {  // attention8.go:262-269
-        vs = vs / 127.0f;
-        vi = 1.0f / vs;
+      for (int u = 0; u < 16; u++)
+        vm = make_float4(fmax32(vm.x, fabsf(vr[u].x)), fmax32(vm.y, fabsf(vr[u].y)),
+                         fmax32(vm.z, fabsf(vr[u].z)), fmax32(vm.w, fabsf(vr[u].w)));
+      for (int t = 16; t < 64; t <<= 1) {
+        vm.x = fmax32(vm.x, __shfl_xor(vm.x, t));
+        vm.y = fmax32(vm.y, __shfl_xor(vm.y, t));
+        vm.z = fmax32(vm.z, __shfl_xor(vm.z, t));
+        vm.w = fmax32(vm.w, __shfl_xor(vm.w, t));
       }
-      mean[tid] = vi;
-      a.vs[((size_t)b * a.nh + h) * D + tid] = vs;
+      if (lane < 16) *(float4 *)&red[wave][4 * sub] = vm;
+      __syncthreads();
+      if (tid < D) {
+        float vs = 0.f;
+        for (int g = 0; g < 8; g++) vs = fmax32(vs, red[g][tid]);
+        float vi = 0.f;
+        if (vs > 0.f) {  // attention8.go:262-269
+          vs = vs / 127.0f;
+          vi = 1.0f / vs;
+        }
+        mean[tid] = vi;
+        a.vs[((size_t)b * a.nh + h) * D + tid] = vs;
+      }
     }
     __syncthreads();
     // quantCols (attention8.go:270-279), 16 keys of a dimension per store
@@ -645,9 +654,11 @@ void launch_attn_quant_q(const AttnArgs &a, hipStream_t s) {
 void launch_attn_prologue(const AttnArgs &a, hipStream_t s) {
   if (a.B <= 0) return;
   if (a.max_n <= kShortSeq) {
-    attn_prologue_short_kernel<<<dim3(a.B, a.nh, 2), 512, 0, s>>>(a);
+    attn_prologue_rows_kernel<false><<<dim3(a.B, a.nh, 2), 512, 0, s>>>(a);
   } else {
-    attn_prologue_kernel<<<dim3(a.B, a.nh), 256, 0, s>>>(a);
+    attn_long_stats_kernel<<<dim3(a.B, a.nh, 8), 256, 0, s>>>(a);
+    const int parts = (a.max_n + kShortSeq - 1) / kShortSeq;
+    attn_prologue_rows_kernel<true><<<dim3(a.B, a.nh, 2 * parts), 512, 0, s>>>(a);
   }
 }
 

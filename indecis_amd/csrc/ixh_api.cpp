@@ -482,7 +482,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
       (rc = w->sa.ensure(4 * (size_t)N)) || (rc = w->qq.ensure((size_t)N * H)) ||
       (rc = w->sq.ensure(4 * (size_t)N * nh)) || (rc = w->kp.ensure((size_t)nh * Npad * D)) ||
       (rc = w->ks.ensure(4 * (size_t)nh * Npad)) || (rc = w->vt.ensure((size_t)nh * D * Npad)) ||
-      (rc = w->vs.ensure(4 * (size_t)B * nh * D)) || (rc = w->ctx.ensure(4 * (size_t)N * H)) ||
+      (rc = w->vs.ensure(3 * 4 * (size_t)B * nh * D)) || (rc = w->ctx.ensure(4 * (size_t)N * H)) ||
       (rc = w->g.ensure(4 * (size_t)N * I)))
     return rc;
 
@@ -600,6 +600,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   aa.ks = w->ks.as<float>();
   aa.vt = w->vt.as<int8_t>();
   aa.vs = w->vs.as<float>();
+  aa.kstat = aa.vs + (size_t)B * nh * D;
   aa.Npad = Npad;
   aa.blocks = w->blocks.as<int32_t>();
   aa.nblocks = nblocks;
@@ -1346,7 +1347,7 @@ int ixh_attend8(int device, float *o, const float *q, const float *k, const floa
       (rc = dblocks.ensure(4 * blocks.size())) || (rc = dqq.ensure((size_t)n * H)) ||
       (rc = dsq.ensure(4 * (size_t)n)) || (rc = dkp.ensure((size_t)Npad * H)) ||
       (rc = dks.ensure(4 * (size_t)Npad)) || (rc = dvt.ensure((size_t)H * Npad)) ||
-      (rc = dvs.ensure(4 * H)) || (rc = dctx.ensure(4 * (size_t)n * H)))
+      (rc = dvs.ensure(3 * 4 * H)) || (rc = dctx.ensure(4 * (size_t)n * H)))
     return rc;
   HIPCK(hipMemcpyAsync(dqkv.p, qkv.data(), 4 * qkv.size(), hipMemcpyHostToDevice, ts.s));
   HIPCK(hipMemcpyAsync(dtabs.p, tabs.data(), 16, hipMemcpyHostToDevice, ts.s));
@@ -1369,6 +1370,7 @@ int ixh_attend8(int device, float *o, const float *q, const float *k, const floa
   aa.ks = dks.as<float>();
   aa.vt = dvt.as<int8_t>();
   aa.vs = dvs.as<float>();
+  aa.kstat = aa.vs + H;
   aa.Npad = Npad;
   aa.blocks = dblocks.as<int32_t>();
   aa.nblocks = (int)blocks.size() / 2;

@@ -108,6 +108,7 @@ struct AttnArgs {
   float *ks;               // [nh][Npad]
   int8_t *vt;              // [nh][64][Npad]
   float *vs;               // [B][nh][64]
+  float *kstat;            // [B][nh][2][64] K mean, 1/V scale (sequences over 512 keys)
   int Npad;
   const int32_t *blocks;   // [nblocks][2]: (sequence, first query)
   int nblocks;

@@ -176,11 +176,13 @@ def test_invalidate_requires_upload():
     m.close()
 
 
-@pytest.mark.parametrize("longest", [512, 513])
+@pytest.mark.parametrize("longest", [512, 513, 1025])
 def test_prologue_edge_lengths(longest):
     """Sequence lengths around the attention prologue's 32-key pieces and
     64-slot padding, with the longest at 512 (single-read prologue) or 513
-    (the two-pass prologue for longer sequences)."""
+    and 1025 (statistics kernel, then 512-key parts; the last part of the
+    longest holds 1 key, and the short sequences of the batch have no
+    second part)."""
     cfg = small_cfg()
     w, gpu, ora = model_pair(cfg, seed=11)
     rng = np.random.default_rng(longest)

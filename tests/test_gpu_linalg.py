@@ -115,7 +115,7 @@ def test_layernorm_quant_exact(m, h, lanes):
 
 @pytest.mark.parametrize("lanes", [8, 16, 0])
 @pytest.mark.parametrize("window", [-1, 8, 64])
-@pytest.mark.parametrize("n", [1, 5, 17, 48, 100, 259, 300, 600])
+@pytest.mark.parametrize("n", [1, 5, 17, 48, 100, 259, 300, 600, 1025, 2600])
 def test_attend8_exact(n, window, lanes):
     """Attend8 on the GPU == the oracle's restatement, bit for bit, with the
     inputs of TestAttend8 (attention8_test.go:50-68)."""
