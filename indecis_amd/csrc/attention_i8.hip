@@ -485,7 +485,7 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   // processes is the same for all its queries and is added to the
   // accumulators per chunk from the prefix sums: O stays exact.
   // P is rounded from the hardware exponential (exp255_fast) unless that
-  // lands within kExp255Tol of a half-integer; there (about 1 score in 500)
+  // lands within kExp255Tol of a half-integer; there (about 1 score in 4000)
   // the reference formula decides: exp32 on the tail keys j >= ts (all keys
   // when lanes = 0), ExpShift's vector formula elsewhere.
   v16i o[2];

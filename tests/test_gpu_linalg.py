@@ -164,8 +164,9 @@ def test_exp255_shortcut_every_float():
     and fall back to the reference formulas (ExpShift's vector body and
     exp32, vec_simd.go:235-262) only near a rounding boundary. Over every
     float v <= 0 the shortcut must never round differently from either
-    formula; its distance from them stays far below the margin."""
+    formula; its distance from them stays below the margin (2^-13, the
+    kernels' kExp255Tol; measured 7.63e-5)."""
     bad_v, bad_s, err_v, err_s, undecided = linalg.check_exp255()
     assert bad_v == 0 and bad_s == 0, (bad_v, bad_s)
-    assert err_v < 2e-4 and err_s < 2e-4, (err_v, err_s)
+    assert err_v < 2.0 ** -13 and err_s < 2.0 ** -13, (err_v, err_s)
     print(f"max |fast - ref|: simd {err_v:.3g}, scalar {err_s:.3g}; undecided floats {undecided}")
