@@ -41,17 +41,6 @@ struct Cfg {
   static constexpr int SMEM = ST * STAGE_BYTES > EPI_TILE_BYTES ? ST * STAGE_BYTES : EPI_TILE_BYTES;
 };
 
-typedef __attribute__((address_space(3))) void *lds_ptr;
-typedef const __attribute__((address_space(1))) void *glb_ptr;
-
-__device__ __forceinline__ int swz(int row) { return (row >> 1) & 3; }
-
-// s_waitcnt with only the vector-memory count (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 // wait until at most `stages` later stages (of L loads each) are in flight
 template <int L>
 __device__ __forceinline__ void wait_stages(int stages) {

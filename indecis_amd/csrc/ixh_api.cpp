@@ -206,8 +206,8 @@ struct RopeTab {
 
 struct Workspace {
   hipStream_t stream = nullptr;
-  DevBuf ids, offs, padoff, pos, blocks, x, xn, qkv, xq, sa, qq, sq, kp, ks, vt, vs, ctx, g,
-      pooled, flag;
+  DevBuf ids, offs, padoff, pos, blocks, seqorder, x, xn, qkv, xq, sa, qq, sq, kp, ks, vt, vs,
+      ctx, g, pooled, flag;
   PinBuf host;
   std::vector<hipEvent_t> events;  // profiling: begin/end pairs, reused
   hipEvent_t order[2] = {nullptr, nullptr};  // cross-stream ordering (no timing)
@@ -473,10 +473,19 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   }
   const int Npad = padoff[B];
   const int nblocks = (int)blocks.size() / 2;
+  // sequences longest first (the fused QKV + prologue kernel's work order)
+  std::vector<int32_t> order(B);
+  for (int b = 0; b < B; b++) order[b] = b;
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int x, int y) { return offs[x + 1] - offs[x] > offs[y + 1] - offs[y]; });
+  // IXH_QKV_FUSED=0: QKV GEMM and attention prologue as two kernels (tests, timing)
+  const char *fe = getenv("IXH_QKV_FUSED");
+  const bool fused = T <= kQkvSeqMax && !(fe && fe[0] == '0');
 
   int rc;
   if ((rc = w->offs.ensure(4 * (B + 1))) || (rc = w->padoff.ensure(4 * (B + 1))) ||
       (rc = w->pos.ensure(4 * (size_t)N)) || (rc = w->blocks.ensure(4 * blocks.size())) ||
+      (rc = w->seqorder.ensure(4 * (size_t)B)) ||
       (rc = w->x.ensure(4 * (size_t)N * H)) || (rc = w->xn.ensure(4 * (size_t)N * H)) ||
       (rc = w->qkv.ensure(4 * (size_t)N * 3 * H)) || (rc = w->xq.ensure((size_t)N * ldq)) ||
       (rc = w->sa.ensure(4 * (size_t)N)) || (rc = w->qq.ensure((size_t)N * H)) ||
@@ -487,16 +496,19 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     return rc;
 
   // small host-built tables through pinned memory
-  const size_t small = 4 * ((B + 1) * 2 + blocks.size());
+  const size_t small = 4 * ((B + 1) * 2 + blocks.size() + B);
   if ((rc = w->host.ensure(small))) return rc;
   int32_t *hs = (int32_t *)w->host.p;
+  int32_t *hs_blocks = hs + 2 * (B + 1), *hs_order = hs_blocks + blocks.size();
   memcpy(hs, offs, 4 * (B + 1));
   memcpy(hs + B + 1, padoff.data(), 4 * (B + 1));
-  if (!blocks.empty()) memcpy(hs + 2 * (B + 1), blocks.data(), 4 * blocks.size());
+  if (!blocks.empty()) memcpy(hs_blocks, blocks.data(), 4 * blocks.size());
+  if (B > 0) memcpy(hs_order, order.data(), 4 * (size_t)B);
   HIPCK(hipMemcpyAsync(w->offs.p, hs, 4 * (B + 1), hipMemcpyHostToDevice, st));
   HIPCK(hipMemcpyAsync(w->padoff.p, hs + B + 1, 4 * (B + 1), hipMemcpyHostToDevice, st));
   if (!blocks.empty())
-    HIPCK(hipMemcpyAsync(w->blocks.p, hs + 2 * (B + 1), 4 * blocks.size(), hipMemcpyHostToDevice, st));
+    HIPCK(hipMemcpyAsync(w->blocks.p, hs_blocks, 4 * blocks.size(), hipMemcpyHostToDevice, st));
+  if (B > 0) HIPCK(hipMemcpyAsync(w->seqorder.p, hs_order, 4 * (size_t)B, hipMemcpyHostToDevice, st));
 
   Pending local;
   Pending &pend = defer ? *defer : local;
@@ -634,12 +646,20 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     g.qq = w->qq.as<int8_t>();
     g.sq = w->sq.as<float>();
     g.attn_scale = aa.scale;
-    RUN("gemm_qkv", 2 * dN * 3 * dH * dH,
-        gemm_bytes(dH, 3 * dH, 2 * dH, false) + dN * (4 + dH + 4 * nh), launch_gemm(EPI_ROPE, g, st));
     // attention (infer.go:437-518)
     aa.window = global ? -1 : c.local_attention / 2;
-    RUN("attn_prologue", 0, dN * 2 * dH * 4 + dN * 2 * dH + 4 * dN * nh,
-        launch_attn_prologue(aa, st));
+    if (fused) {
+      // QKV GEMM and Attn8.Prepare in one kernel: int8 Q, K, V and their
+      // scales are its only outputs
+      RUN("gemm_qkv", 2 * dN * 3 * dH * dH,
+          gemm_bytes(dH, 3 * dH, 0, false) + dN * (3 * dH + 8 * nh) + 4.0 * B * dH,
+          launch_qkv_attn(g, aa, w->seqorder.as<int32_t>(), st));
+    } else {
+      RUN("gemm_qkv", 2 * dN * 3 * dH * dH,
+          gemm_bytes(dH, 3 * dH, 2 * dH, false) + dN * (4 + dH + 4 * nh), launch_gemm(EPI_ROPE, g, st));
+      RUN("attn_prologue", 0, dN * 2 * dH * 4 + dN * 2 * dH + 4 * dN * nh,
+          launch_attn_prologue(aa, st));
+    }
     const double pairs = global ? keys_global : keys_local;
     RUN(global ? "attn_global" : "attn_local", 4.0 * D * nh * pairs,
         dN * 3 * dH + 8 * dN * nh + dN * dH * 4, launch_attn_main(aa, st));

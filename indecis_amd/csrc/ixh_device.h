@@ -131,6 +131,21 @@ __device__ __forceinline__ float gelu_scalar(float x) {
   return 0.5f * x * (1.0f + p / q);
 }
 
+// Direct-to-LDS loads (global_load_lds_dwordx4): pointer types, and the
+// XOR swizzle of the four 16-byte chunks of a 64-byte LDS row, by
+// (row >> 1) & 3, so 16-byte fragment reads of consecutive rows fall in
+// distinct banks.
+typedef __attribute__((address_space(3))) void *lds_ptr;
+typedef const __attribute__((address_space(1))) void *glb_ptr;
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 3; }
+
+// s_waitcnt with only the vector-memory count (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // Dequantisation of one int8 GEMM result (kernel_vnni_amd64.s:144-200):
 // f32(tile) - zc, times sb, times sa — tile being the reference's
 // unsigned-offset integer sum.

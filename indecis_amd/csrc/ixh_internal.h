@@ -125,4 +125,12 @@ void launch_check_exp255(uint32_t lo, uint32_t hi, unsigned long long *res, hipS
 constexpr int kAttnQBlock = 128;  // queries per workgroup (4 waves x 32)
 constexpr int kKeyPad = 64;       // key slots of a sequence are padded to this
 
+// The QKV projection fused with the attention prologue (qkv_attn.hip), for
+// batches whose sequences have at most kQkvSeqMax keys: g as for the
+// EPI_ROPE GEMM (A, sa, B, sb, zc, c128, Kp, rope tables, pos, qq, sq,
+// attn_scale; C unused), a as for launch_attn_prologue (qkv unused);
+// order[B]: the sequences, longest first.
+constexpr int kQkvSeqMax = 512;
+void launch_qkv_attn(const GemmArgs &g, const AttnArgs &a, const int32_t *order, hipStream_t s);
+
 }  // namespace ixh

@@ -1,0 +1,369 @@
+// qkv_attn.hip — the QKV projection fused with the attention prologue, for
+// batches whose sequences have at most kQkvSeqMax keys.
+//
+// One workgroup per (sequence, head, Q|K|V) computes the 64 output columns
+// of that head's Q, K or V over all rows of the sequence (the int8 GEMM of
+// gemm_i8.hip: i8 MFMA, exact int32 sums, the reference's dequantisation,
+// RoPE on Q and K) and finishes Attn8.Prepare (attention8.go:203-280) on
+// them in place, so neither K nor V goes through HBM in float32:
+//  Q: quantised per (row, head), 1/sqrt(D) folded into the scale
+//     (attention8.go:211-220);
+//  K: the float32 mean over the sequence — 64 sequential sums in key order
+//     (AddTo, attention8.go:224-228) run by one wave over LDS slabs of 256
+//     keys — then centred and quantised per key (attention8.go:240-251);
+//  V: max |V| per dimension (MaxAbsTo, attention8.go:259-269), then
+//     quantised per dimension and stored transposed (attention8.go:270-279).
+// The outputs are those of the QKV GEMM (EPI_ROPE, queries) plus
+// launch_attn_prologue: qq, sq, kp, ks, vt, vs, same layouts, same bits.
+//
+// Layout: 8 waves; 32-row block rb of the sequence (rb < 16) belongs to
+// wave rb % 8, which holds it as 2 MFMA 32x32 tiles (the head's 64
+// columns). K steps of 64 stream A (the sequence's rows, up to 32 KB) and
+// B (the head's 64 weight rows, 4 KB) into a 2-stage LDS ring with
+// direct-to-LDS loads, as the GEMM does. Workgroups are dealt so that the
+// 36 of a sequence (12 heads x Q, K, V) run on one XCD and share its rows
+// in L2; sequences go longest first, spread over the 8 XCDs.
+#include "ixh_device.h"
+#include "ixh_internal.h"
+
+namespace ixh {
+
+namespace {
+
+constexpr int D = 64, BK = 64, NXCD = 8;
+constexpr int SEQ_MAX = kQkvSeqMax;           // 512 rows
+constexpr int A_BYTES = SEQ_MAX * BK;         // A part of a stage
+constexpr int STAGE = A_BYTES + D * BK;       // + B part
+constexpr int KT_LD = 68;                     // floats per row of the Q/K slab
+constexpr int SLAB_BYTES = 256 * KT_LD * 4;   // 256 keys
+constexpr int SMEM = 2 * STAGE > SLAB_BYTES ? 2 * STAGE : SLAB_BYTES;
+constexpr int VT_LD = 48;                     // bytes per dimension of the V^T staging tile
+
+__global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a, const int32_t *order) {
+  extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+  __shared__ float sa_s[SEQ_MAX];
+  __shared__ float red_s[8][D];
+  __shared__ __attribute__((aligned(16))) float stat_s[D];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int per_seq = 3 * a.nh;
+  const int xcd = blockIdx.x % NXCD, k = blockIdx.x / NXCD;
+  const int si = xcd + NXCD * (k / per_seq);
+  if (si >= a.B) return;
+  const int b = order[si];
+  const int part = (k % per_seq) / a.nh, h = (k % per_seq) % a.nh;
+  const int base = a.offs[b], n = a.offs[b + 1] - base;
+  const int npad = (n + kKeyPad - 1) / kKeyPad * kKeyPad;
+  const int nb = npad / 32;  // 32-row blocks (even, at most 16)
+  const int col0 = part * a.H + h * D;  // the head's first output column
+  if (n == 0) {
+    if (part == 2 && tid < D) a.vs[((size_t)b * a.nh + h) * D + tid] = 0.f;
+    return;
+  }
+  for (int t = tid; t < 32 * nb; t += 512) sa_s[t] = g.sa[base + min(t, n - 1)];
+
+  // ---- int8 GEMM of the sequence's rows by the head's 64 weight rows ----
+  // Stage chunks of 16 rows x 64 bytes (one wave instruction each): A
+  // chunks 0 .. 2nb-1 (rows past n load row n-1, never stored), then the 4
+  // B chunks; chunk q is loaded by wave q % 8. Lane i fills 16 bytes of its
+  // chunk: row i/4, physical 16-byte column i%4 (logical (i%4) ^ swz).
+  const int lrow = lane >> 2, lchunk = (lane & 3) ^ swz(lane >> 2);
+  const int nchunk = 2 * nb + 4;
+  auto issue = [&](int kt) {
+    int8_t *st = smem + (kt & 1) * STAGE;
+    const int k0 = kt * BK + 16 * lchunk;
+    for (int q = wave; q < nchunk; q += 8) {
+      if (q < 2 * nb) {
+        const int row = min(16 * q + lrow, n - 1);
+        __builtin_amdgcn_global_load_lds((glb_ptr)(g.A + (size_t)(base + row) * g.lda + k0),
+                                         (lds_ptr)(st + 16 * q * BK), 16, 0, 0);
+      } else {
+        const int qb = q - 2 * nb;
+        __builtin_amdgcn_global_load_lds((glb_ptr)(g.B + (size_t)(col0 + 16 * qb + lrow) * g.ldb + k0),
+                                         (lds_ptr)(st + A_BYTES + 16 * qb * BK), 16, 0, 0);
+      }
+    }
+  };
+
+  v16i acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+  const int nk = g.Kp / BK;
+  issue(0);
+  for (int kt = 0; kt < nk; kt++) {
+    // this step's loads landed (nothing else is in flight), every wave's
+    // too after the barrier; the other stage is free
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (kt + 1 < nk) issue(kt + 1);
+    const int8_t *st = smem + (kt & 1) * STAGE;
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      v4i fb[2];
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int row = 32 * j + fr;
+        fb[j] = *(const v4i *)(st + A_BYTES + row * BK + 16 * ((2 * s + fh) ^ swz(row)));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        if (wave + 8 * i < nb) {
+          const int row = 32 * (wave + 8 * i) + fr;
+          const v4i fa = *(const v4i *)(st + row * BK + 16 * ((2 * s + fh) ^ swz(row)));
+#pragma unroll
+          for (int j = 0; j < 2; j++) acc[i][j] = mfma32(fa, fb[j], acc[i][j]);
+        }
+      }
+    }
+  }
+  __syncthreads();  // the ring is no longer read
+
+  // ---- dequantisation (and RoPE on Q and K) in the MFMA layout ----
+  // lane: columns fr and 32 + fr of the head, rows 32 rb + acc_row(r)
+  float zc[2], sb[2];
+  int c128[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int nc = col0 + 32 * j + fr;
+    zc[j] = g.zc[nc];
+    sb[j] = g.sb[nc];
+    c128[j] = g.c128[nc];
+  }
+  float v[2][2][16];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    if (wave + 8 * i >= nb) continue;
+    // RoPE tables (cos, sin: 32 floats a position) of the block's 32 rows,
+    // staged into this wave's 8 KB of the free ring by 8 direct-to-LDS
+    // loads; a row's position is its index in the sequence (padding rows:
+    // n-1)
+    const float *tab = (const float *)(smem + wave * 8192);
+    if (part < 2) {
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int p = min(32 * (wave + 8 * i) + 8 * u + (lane >> 3), n - 1);
+        const size_t off = (size_t)p * 32 + 4 * (lane & 7);
+        __builtin_amdgcn_global_load_lds((glb_ptr)(g.rope_cos + off), (lds_ptr)(smem + wave * 8192 + 1024 * u), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((glb_ptr)(g.rope_sin + off),
+                                         (lds_ptr)(smem + wave * 8192 + 4096 + 1024 * u), 16, 0, 0);
+      }
+      wait_vmcnt<0>();
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = 32 * (wave + 8 * i) + acc_row(r, lane);
+      const float sa = sa_s[row];
+      float v0 = deq(acc[i][0][r] + c128[0], zc[0], sb[0], sa);
+      float v1 = deq(acc[i][1][r] + c128[1], zc[1], sb[1], sa);
+      if (part < 2) {
+        // linalg.Rope (vec_simd.go:408-425): x1' = x1*c - x2*s, x2' = x2*c + x1*s
+        const float c = tab[acc_row(r, lane) * 32 + fr], sn = tab[1024 + acc_row(r, lane) * 32 + fr];
+        const float x1 = v0, x2 = v1;
+        v0 = x1 * c - x2 * sn;
+        v1 = x2 * c + x1 * sn;
+      }
+      v[i][0][r] = v0;
+      v[i][1][r] = v1;
+    }
+  }
+  __syncthreads();  // every wave is done with its tables: the ring is free again
+
+  if (part == 2) {
+    // ---- V: max |V| per dimension, scale, quantCols, V^T ----
+    float vm[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      if (wave + 8 * i >= nb) continue;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        if (32 * (wave + 8 * i) + acc_row(r, lane) < n) {
+          vm[0] = fmax32(vm[0], fabsf(v[i][0][r]));
+          vm[1] = fmax32(vm[1], fabsf(v[i][1][r]));
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      vm[j] = fmax32(vm[j], __shfl_xor(vm[j], 32));
+      if (fh == 0) red_s[wave][32 * j + fr] = vm[j];
+    }
+    __syncthreads();
+    if (tid < D) {
+      float vs = 0.f;
+      for (int w = 0; w < 8; w++) vs = fmax32(vs, red_s[w][tid]);
+      float vi = 0.f;
+      if (vs > 0.f) {  // attention8.go:262-269
+        vs = vs / 127.0f;
+        vi = 1.0f / vs;
+      }
+      a.vs[((size_t)b * a.nh + h) * D + tid] = vs;
+      stat_s[tid] = vi;
+    }
+    __syncthreads();
+    const float vi0 = stat_s[fr], vi1 = stat_s[32 + fr];
+    int8_t *vt_s = smem + wave * (D * VT_LD);  // [64 dims][32 keys] of this wave's block
+    int8_t *vt = a.vt + (size_t)h * D * a.Npad + a.padoff[b];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int rb = wave + 8 * i;
+      if (rb < nb) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+#pragma unroll
+          for (int gq = 0; gq < 4; gq++) {
+            int qv[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+              const int r = 4 * gq + u;
+              qv[u] = 32 * rb + acc_row(r, lane) < n ? q8(v[i][j][r], j ? vi1 : vi0) : 0;
+            }
+            // keys 8gq + 4fh + 0..3 of dimension 32j + fr
+            *(int *)(vt_s + (32 * j + fr) * VT_LD + 8 * gq + 4 * fh) =
+                (qv[0] & 0xff) | ((qv[1] & 0xff) << 8) | ((qv[2] & 0xff) << 16) | (qv[3] << 24);
+          }
+        }
+      }
+      __syncthreads();
+      if (rb < nb) {
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+          *(v4i *)(vt + (size_t)lane * a.Npad + 32 * rb + 16 * u) = *(const v4i *)(vt_s + lane * VT_LD + 16 * u);
+      }
+      __syncthreads();
+    }
+    return;
+  }
+
+  // ---- Q and K: rows through an LDS slab of 256 rows ----
+  // PUT(t): this wave's block of round t (rows 256t + 32 wave ..) into the
+  // slab, in the MFMA layout
+  float *slab = (float *)smem;  // [256 rows][KT_LD]
+#define PUT(t)                                                    \
+  if (wave + 8 * (t) < nb) {                                      \
+    _Pragma("unroll") for (int r = 0; r < 16; r++) {              \
+      const int lr = 32 * wave + acc_row(r, lane);                \
+      slab[lr * KT_LD + fr] = v[t][0][r];                         \
+      slab[lr * KT_LD + 32 + fr] = v[t][1][r];                    \
+    }                                                             \
+  }
+  if (part == 1) {
+    // K mean over the sequence: 64 float32 chains in key order, one lane
+    // a dimension
+    float ksum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      if (256 * t < n) {  // block-uniform
+        PUT(t)
+        __syncthreads();
+        if (wave == 0) {
+          const int cnt = min(256, n - 256 * t);
+          for (int lr = 0; lr < cnt; lr++) ksum = ksum + slab[lr * KT_LD + lane];
+        }
+        __syncthreads();
+      }
+    }
+    if (wave == 0) stat_s[lane] = ksum * (1.0f / (float)n);  // Scale(mean, 1/n)
+    __syncthreads();
+  }
+
+  // Per-row quantisation of the slab's rows (round t): two threads a row,
+  // 32 values each (thread: row 16 (lane / 32) + lane % 16 of its wave's
+  // 32, half (lane / 16) % 2), K centred first (quantRowAVX2 without the
+  // flip, attention8.go:240-251), Q as Attn8.Prepare quantises queries
+  // (attention8.go:211-220).
+  int8_t *kp = a.kp + ((size_t)h * a.Npad + a.padoff[b]) * D;
+  float *ks = a.ks + (size_t)h * a.Npad + a.padoff[b];
+  const int hh = (lane >> 4) & 1;
+  const int lr = 32 * wave + 16 * (lane >> 5) + (lane & 15);
+  auto quant_round = [&](int t) {
+    const int row = 256 * t + lr;
+    const float4 *src = (const float4 *)(slab + lr * KT_LD + 32 * hh);
+    const float4 *mu = (const float4 *)(stat_s + 32 * hh);
+    // the slab is read twice (max, then quantisation): fewer live registers
+    auto value = [&](int c) {
+      float4 x = src[c];
+      if (part == 1) {
+        const float4 m4 = mu[c];
+        x = make_float4(x.x - m4.x, x.y - m4.y, x.z - m4.z, x.w - m4.w);
+      }
+      return x;
+    };
+    float mx = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const float4 x = value(c);
+      mx = fmax32(mx, fmax32(fmax32(fabsf(x.x), fabsf(x.y)), fmax32(fabsf(x.z), fabsf(x.w))));
+    }
+    mx = fmax32(mx, __shfl_xor(mx, 16));
+    __asm__ volatile("" ::: "memory");  // keep the second read of the slab
+    float sc = 0.f, inv = 0.f;
+    if (mx != 0.f) {
+      sc = mx / 127.0f;
+      inv = 1.0f / sc;
+    }
+    const bool valid = row < n;
+    int w[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const float4 x = value(c);
+      w[c] = valid ? (q8(x.x, inv) & 0xff) | ((q8(x.y, inv) & 0xff) << 8) | ((q8(x.z, inv) & 0xff) << 16) |
+                         (q8(x.w, inv) << 24)
+                   : 0;
+    }
+    const v4i lo = {w[0], w[1], w[2], w[3]}, hi = {w[4], w[5], w[6], w[7]};
+    if (part == 0) {
+      if (valid) {
+        int8_t *dst = g.qq + (size_t)(base + row) * a.H + h * D + 32 * hh;
+        *(v4i *)dst = lo;
+        *(v4i *)(dst + 16) = hi;
+        if (hh == 0) g.sq[(size_t)(base + row) * a.nh + h] = sc * g.attn_scale;
+      }
+    } else if (row < npad) {
+      int8_t *dst = kp + (size_t)row * D + 32 * hh;
+      *(v4i *)dst = lo;
+      *(v4i *)(dst + 16) = hi;
+      if (hh == 0) ks[row] = valid ? sc : 0.f;
+    }
+  };
+  if (part == 1) {
+    // the slab holds the chains' last round
+    if (n > 256) {
+      quant_round(1);
+      __syncthreads();
+      PUT(0)
+      __syncthreads();
+    }
+    quant_round(0);
+  } else {
+    PUT(0)
+    __syncthreads();
+    quant_round(0);
+    if (n > 256) {
+      __syncthreads();
+      PUT(1)
+      __syncthreads();
+      quant_round(1);
+    }
+  }
+#undef PUT
+}
+
+}  // namespace
+
+void launch_qkv_attn(const GemmArgs &g, const AttnArgs &a, const int32_t *order, hipStream_t s) {
+  if (a.B <= 0) return;
+  const int grid = NXCD * 3 * a.nh * ((a.B + NXCD - 1) / NXCD);
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void *)qkv_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
+    attr_set = true;
+  }
+  qkv_attn_kernel<<<grid, 512, SMEM, s>>>(g, a, order);
+}
+
+}  // namespace ixh
