@@ -54,7 +54,8 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
   const int part = (k % per_seq) / a.nh, h = (k % per_seq) % a.nh;
   const int base = a.offs[b], n = a.offs[b + 1] - base;
   const int npad = (n + kKeyPad - 1) / kKeyPad * kKeyPad;
-  const int nb = npad / 32;  // 32-row blocks (even, at most 16)
+  const int nb = npad / 32;            // 32-row blocks stored (even, at most 16)
+  const int nbc = (n + 31) / 32;       // blocks computed: a block past n is all zeros
   const int col0 = part * a.H + h * D;  // the head's first output column
   if (n == 0) {
     if (part == 2 && tid < D) a.vs[((size_t)b * a.nh + h) * D + tid] = 0.f;
@@ -64,21 +65,21 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
 
   // ---- int8 GEMM of the sequence's rows by the head's 64 weight rows ----
   // Stage chunks of 16 rows x 64 bytes (one wave instruction each): A
-  // chunks 0 .. 2nb-1 (rows past n load row n-1, never stored), then the 4
-  // B chunks; chunk q is loaded by wave q % 8. Lane i fills 16 bytes of its
-  // chunk: row i/4, physical 16-byte column i%4 (logical (i%4) ^ swz).
+  // chunks 0 .. 2nbc-1 (rows past n load row n-1, never stored), then the
+  // 4 B chunks; chunk q is loaded by wave q % 8. Lane i fills 16 bytes of
+  // its chunk: row i/4, physical 16-byte column i%4 (logical (i%4) ^ swz).
   const int lrow = lane >> 2, lchunk = (lane & 3) ^ swz(lane >> 2);
-  const int nchunk = 2 * nb + 4;
+  const int nchunk = 2 * nbc + 4;
   auto issue = [&](int kt) {
     int8_t *st = smem + (kt & 1) * STAGE;
     const int k0 = kt * BK + 16 * lchunk;
     for (int q = wave; q < nchunk; q += 8) {
-      if (q < 2 * nb) {
+      if (q < 2 * nbc) {
         const int row = min(16 * q + lrow, n - 1);
         __builtin_amdgcn_global_load_lds((glb_ptr)(g.A + (size_t)(base + row) * g.lda + k0),
                                          (lds_ptr)(st + 16 * q * BK), 16, 0, 0);
       } else {
-        const int qb = q - 2 * nb;
+        const int qb = q - 2 * nbc;
         __builtin_amdgcn_global_load_lds((glb_ptr)(g.B + (size_t)(col0 + 16 * qb + lrow) * g.ldb + k0),
                                          (lds_ptr)(st + A_BYTES + 16 * qb * BK), 16, 0, 0);
       }
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
       }
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        if (wave + 8 * i < nb) {
+        if (wave + 8 * i < nbc) {
           const int row = 32 * (wave + 8 * i) + fr;
           const v4i fa = *(const v4i *)(st + row * BK + 16 * ((2 * s + fh) ^ swz(row)));
 #pragma unroll
