@@ -124,6 +124,27 @@ int ixh_encode_tokens(ixh_model *m, const int32_t *ids, const int32_t *offs,
 int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs,
                       int B, int out_kind, float *d_out, void *stream);
 
+/* WithBatching (model.go:136-160) and its batcher (batch.go:1-82): requests
+ * from concurrent callers are grouped into one encode pass. `workers`
+ * threads each take the first pending request and, without waiting, those
+ * already queued while the batch stays under `max_rows` tokens; the
+ * sequences go end to end and each request gets its pooled rows. An error
+ * of the pass (an id out of vocabulary) is returned to every request of
+ * that batch. workers <= 0: 2; max_rows <= 0: 65536 (the reference's CPU
+ * default, 512, is far below what fills the GPU). */
+typedef struct ixh_batcher ixh_batcher;
+int ixh_batcher_create(ixh_model *m, int workers, int max_rows, ixh_batcher **out);
+/* batcher.encode (batch.go:32-49): EncodeSeqs's arguments; blocks until
+ * the request's pooled rows [B][H] are in out. Thread-safe. */
+int ixh_batcher_encode(ixh_batcher *b, const int32_t *ids, const int32_t *offs,
+                       int B, float *out);
+/* Passes run and requests served so far (no counterpart in the reference;
+ * for tests and serving metrics). */
+int ixh_batcher_stats(ixh_batcher *b, int64_t *batches, int64_t *requests);
+/* Waits for queued requests, stops the workers, frees the batcher. The
+ * model must outlive it. */
+void ixh_batcher_destroy(ixh_batcher *b);
+
 /* Per-kernel timing (no counterpart in the reference, whose profiling is Go
  * pprof around the whole call, tools/infbench/main.go:71-88): when on,
  * every kernel of an encode is bracketed by HIP events on its stream and

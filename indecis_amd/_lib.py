@@ -20,7 +20,8 @@ EXPORTS = [
     "ixh_head_logits", "ixh_packb8_create", "ixh_packb8_destroy", "ixh_matmul8",
     "ixh_matmul8_tile", "ixh_layernorm_quant", "ixh_ln_matmul8_geglu", "ixh_attend8",
     "ixh_model_set_profiling", "ixh_model_set_profile_filter", "ixh_model_profile",
-    "ixh_check_exp255",
+    "ixh_check_exp255", "ixh_batcher_create", "ixh_batcher_encode", "ixh_batcher_stats",
+    "ixh_batcher_destroy",
 ]
 
 IXH_OK, IXH_EINVAL, IXH_ERANGE, IXH_ESTATE, IXH_EHIP, IXH_ENOMEM = range(6)
@@ -93,6 +94,9 @@ def lib():
         "ixh_model_profile": [vp, C.POINTER(IxhKernelStat), C.c_int, C.POINTER(C.c_int)],
         "ixh_check_exp255": [C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_float),
                              C.POINTER(C.c_int64)],
+        "ixh_batcher_create": [vp, C.c_int, C.c_int, C.POINTER(vp)],
+        "ixh_batcher_encode": [vp, vp, vp, C.c_int, vp],
+        "ixh_batcher_stats": [vp, C.POINTER(C.c_int64), C.POINTER(C.c_int64)],
     }
     for name, args in sig.items():
         f = getattr(L, name)
@@ -102,6 +106,8 @@ def lib():
     L.ixh_model_destroy.restype = None
     L.ixh_packb8_destroy.argtypes = [vp]
     L.ixh_packb8_destroy.restype = None
+    L.ixh_batcher_destroy.argtypes = [vp]
+    L.ixh_batcher_destroy.restype = None
     _lib = L
     return L
 

@@ -13,7 +13,10 @@
 #include <cstring>
 #include <memory>
 #include <mutex>
+#include <condition_variable>
+#include <deque>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/indecis_hip.h"
@@ -1430,6 +1433,142 @@ int ixh_check_exp255(int device, int64_t bad[2], float max_err[2], int64_t *unde
   memcpy(&max_err[1], &e1, 4);
   *undecided = (int64_t)r[4];
   return IXH_OK;
+}
+
+}  // extern "C"
+
+// ---- batching of concurrent requests ----------------------------------------
+// WithBatching / batcher (batch.go:1-82, model.go:136-160): worker threads
+// each take the first pending request and, without waiting, the requests
+// already queued while the batch stays under max_rows tokens, run them as
+// one encode pass (sequences end to end), and hand every request its
+// pooled rows; an error of the pass goes to every request of the batch.
+namespace {
+struct BatchReq {
+  const int32_t *ids;
+  const int32_t *offs;
+  int B, rows;
+  float *out;
+  int rc = IXH_OK;
+  std::string err;
+  bool done = false;
+};
+}  // namespace
+
+struct ixh_batcher {
+  ixh_model *m = nullptr;
+  int max_rows = 0;
+  std::mutex mu;
+  std::condition_variable work_cv, done_cv;
+  std::deque<BatchReq *> queue;
+  bool stop = false;
+  int64_t batches = 0, requests = 0;
+  std::vector<std::thread> workers;
+};
+
+namespace {
+// batcher.work (batch.go:51-82)
+void batcher_work(ixh_batcher *b) {
+  const int H = b->m->cfg.hidden;
+  std::vector<BatchReq *> batch;
+  std::vector<int32_t> ids, offs;
+  std::vector<float> pooled;
+  for (;;) {
+    batch.clear();
+    {
+      std::unique_lock<std::mutex> lk(b->mu);
+      b->work_cv.wait(lk, [&] { return b->stop || !b->queue.empty(); });
+      if (b->queue.empty()) return;  // closed and drained
+      batch.push_back(b->queue.front());
+      b->queue.pop_front();
+      int rows = batch[0]->rows;
+      while (rows < b->max_rows && !b->queue.empty()) {
+        batch.push_back(b->queue.front());
+        rows += b->queue.front()->rows;
+        b->queue.pop_front();
+      }
+    }
+    int B = 0;
+    for (BatchReq *r : batch) B += r->B;
+    offs.assign(B + 1, 0);
+    ids.clear();
+    int k = 0;
+    for (BatchReq *r : batch) {
+      ids.insert(ids.end(), r->ids, r->ids + r->offs[r->B]);
+      for (int s = 0; s < r->B; s++, k++) offs[k + 1] = offs[k] + (r->offs[s + 1] - r->offs[s]);
+    }
+    pooled.resize((size_t)B * H);
+    const int rc = encode_host(b->m, ids.data(), offs.data(), B, IXH_OUT_POOLED, pooled.data());
+    size_t off = 0;
+    for (BatchReq *r : batch) {
+      if (rc) {
+        r->rc = rc;
+        r->err = g_err;
+      } else {
+        memcpy(r->out, pooled.data() + off, sizeof(float) * (size_t)r->B * H);
+      }
+      off += (size_t)r->B * H;
+    }
+    {
+      std::lock_guard<std::mutex> lk(b->mu);
+      for (BatchReq *r : batch) r->done = true;
+      b->batches++;
+      b->requests += (int64_t)batch.size();
+    }
+    b->done_cv.notify_all();
+  }
+}
+}  // namespace
+
+extern "C" {
+
+int ixh_batcher_create(ixh_model *m, int workers, int max_rows, ixh_batcher **out) {
+  if (!m || !out) return fail(IXH_EINVAL, "modernbert: nil model");
+  if (workers <= 0) workers = 2;
+  if (max_rows <= 0) max_rows = 65536;
+  ixh_batcher *b = new ixh_batcher;
+  b->m = m;
+  b->max_rows = max_rows;
+  for (int i = 0; i < workers; i++) b->workers.emplace_back(batcher_work, b);
+  *out = b;
+  return IXH_OK;
+}
+
+int ixh_batcher_encode(ixh_batcher *b, const int32_t *ids, const int32_t *offs, int B, float *out) {
+  if (!b) return fail(IXH_EINVAL, "modernbert: nil batcher");
+  int rc;
+  if ((rc = check_offs(offs, B))) return rc;
+  if (B == 0) return IXH_OK;
+  if ((offs[B] > 0 && !ids) || !out) return fail(IXH_EINVAL, "modernbert: inconsistent batch");
+  BatchReq r{ids, offs, B, offs[B], out};
+  {
+    std::unique_lock<std::mutex> lk(b->mu);
+    if (b->stop) return fail(IXH_EINVAL, "modernbert: batcher closed");
+    b->queue.push_back(&r);
+    b->work_cv.notify_one();
+    b->done_cv.wait(lk, [&] { return r.done; });
+  }
+  if (r.rc) return fail(r.rc, "%s", r.err.c_str());
+  return IXH_OK;
+}
+
+int ixh_batcher_stats(ixh_batcher *b, int64_t *batches, int64_t *requests) {
+  if (!b || !batches || !requests) return fail(IXH_EINVAL, "modernbert: nil batcher");
+  std::lock_guard<std::mutex> lk(b->mu);
+  *batches = b->batches;
+  *requests = b->requests;
+  return IXH_OK;
+}
+
+void ixh_batcher_destroy(ixh_batcher *b) {
+  if (!b) return;
+  {
+    std::lock_guard<std::mutex> lk(b->mu);
+    b->stop = true;
+  }
+  b->work_cv.notify_all();
+  for (std::thread &t : b->workers) t.join();
+  delete b;
 }
 
 }  // extern "C"

@@ -304,3 +304,42 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+class Batcher:
+    """WithBatching (model.go:136-160) / batcher (batch.go): encode_seqs
+    calls from concurrent threads are grouped into single encode passes of
+    up to max_rows tokens by `workers` native threads (0: library
+    defaults, 2 workers and 65536 tokens). The model must outlive it."""
+
+    def __init__(self, model, workers=0, max_rows=0):
+        self.model = model
+        self._L = model._L
+        h = C.c_void_p()
+        _lib.check(self._L.ixh_batcher_create(model._h, workers, max_rows, C.byref(h)))
+        self._h = h
+
+    def encode_seqs(self, seqs):
+        """batcher.encode (batch.go:32-49): [B, H] pooled embeddings; an
+        error of the pass the request joined is raised here."""
+        ids, offs = _offsets(seqs)
+        out = np.zeros((max(len(seqs), 1), self.model.cfg.hidden), np.float32)
+        _lib.check(self._L.ixh_batcher_encode(self._h, _ptr(ids), _ptr(offs), len(seqs), _ptr(out)))
+        return out[:len(seqs)]
+
+    def stats(self):
+        """(passes run, requests served) so far."""
+        b, r = C.c_int64(0), C.c_int64(0)
+        _lib.check(self._L.ixh_batcher_stats(self._h, C.byref(b), C.byref(r)))
+        return b.value, r.value
+
+    def close(self):
+        if self._h:
+            self._L.ixh_batcher_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -193,6 +193,20 @@ def test_prologue_edge_lengths(longest):
     assert f32_bits_equal(got, want), mismatch_report(got, want)
 
 
+def test_unfused_qkv_path_exact(monkeypatch):
+    """IXH_QKV_FUSED=0: a batch of short sequences through the QKV GEMM
+    (float32 K, V) and the separate attention prologue, the path every
+    batch with a sequence over 512 keys takes, equals the oracle too."""
+    monkeypatch.setenv("IXH_QKV_FUSED", "0")
+    cfg = small_cfg(layers=3)
+    w, gpu, ora = model_pair(cfg, seed=23)
+    rng = np.random.default_rng(23)
+    seqs = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32) for n in (1, 33, 64, 65, 300, 512, 0, 7)]
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+
+
 @pytest.mark.parametrize("parts", ["2", "3"])
 def test_split_streams_exact(parts, monkeypatch):
     """A batch of at least 4,096 tokens runs as parts on as many streams
