@@ -85,6 +85,53 @@ def load_traffic(kernel, workload):
     return d.get("hbm_bytes_per_launch")
 
 
+def serving(np, model, cfg, args):
+    """WithBatching under load (model.go:136-160): `clients` threads each
+    send `requests` requests of one sequence (U[16,128] tokens, host ids in,
+    pooled row out), first as direct concurrent EncodeSeqs calls, then
+    through the batcher; one JSON line with both rates."""
+    import threading
+    from indecis_amd.modernbert import Batcher
+    rng = np.random.default_rng(7)
+    reqs = [[rng.integers(0, cfg.vocab, size=int(rng.integers(16, 129)), dtype=np.int32)]
+            for _ in range(args.clients * args.requests)]
+    tokens = sum(len(r[0]) for r in reqs)
+
+    def run(fn):
+        def burst(step):
+            def client(k):
+                for i in range(k, len(reqs), step):
+                    fn(reqs[i])
+            ts = [threading.Thread(target=client, args=(k,)) for k in range(args.clients)]
+            t0 = time.perf_counter()
+            for t in ts:
+                t.start()
+            for t in ts:
+                t.join()
+            return time.perf_counter() - t0
+        burst(len(reqs))  # warm-up: one request per client, concurrently (workspaces)
+        return burst(args.clients)
+
+    direct = run(model.encode_seqs)
+    bat = Batcher(model)
+    batched = run(bat.encode_seqs)
+    passes, served = bat.stats()
+    bat.close()
+    n = len(reqs)
+    print(json.dumps({
+        "metric": "serving: single-sequence requests/s from concurrent clients",
+        "unit": "requests/s", "higher_is_better": True, "n_gpus": 1, "data": "synthetic",
+        "config": {"workload": f"ModernBERT-{'base' if cfg.hidden == 768 else 'small'}-shaped int8 encoder, "
+                               f"{args.clients} client threads x {args.requests} requests of 1 sequence "
+                               f"(U[16,128] tokens), pooled output to the host",
+                   "requests": n, "tokens": tokens},
+        "direct": {"value": round(n / direct, 1), "tokens_per_s": round(tokens / direct, 1)},
+        "batcher": {"value": round(n / batched, 1), "tokens_per_s": round(tokens / batched, 1),
+                    "requests_per_pass": round(served / max(passes, 1), 2),
+                    "note": "library defaults: 2 workers, 65536 tokens per pass"},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -98,6 +145,10 @@ def main():
                     help="run every phase with the batch in this many parts (profiling runs: 1)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one device copy of 512 MiB (PMC calibration)")
+    ap.add_argument("--serving", action="store_true",
+                    help="instead: concurrent single-sequence requests, direct calls vs the batcher")
+    ap.add_argument("--clients", type=int, default=32)
+    ap.add_argument("--requests", type=int, default=40, help="requests per client (--serving)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -121,6 +172,10 @@ def main():
 
     torch.cuda.set_device(0)
     model = Model(weights, device=0, lanes=args.lanes)
+    if args.serving:
+        serving(np, model, cfg, args)
+        model.close()
+        return
     ids_d = torch.from_numpy(np.concatenate(seqs)).to("cuda")
     out_d = torch.empty((B, cfg.hidden), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
