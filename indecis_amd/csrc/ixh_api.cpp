@@ -108,11 +108,13 @@ struct DeviceGuard {
     return fail(IXH_EHIP, "modernbert: hip: %s (hipSetDevice %d)", hipGetErrorString(dg_.err), dev);
 
 // A quantised weight matrix on the device, padded to the GEMM tiles:
-// rows to a multiple of 128 (zero channels), depth to a multiple of 64.
+// rows to a multiple of 256 (zero channels), depth to a multiple of 64.
+// q holds it row-major [np][kp] (gemm_i8, the fused QKV kernel), qk the same
+// bytes K-blocked [kp/32][np][32] (gemm_as: one MFMA operand is 1 KB).
 struct Mat {
   int k = 0, n = 0, kp = 0, np = 0;
   bool set = false;
-  DevBuf q, sb, zc, c128;
+  DevBuf q, qk, sb, zc, c128;
 };
 
 // Rows [n][k] from either layout.
@@ -136,7 +138,7 @@ int upload_mat(Mat &M, const std::vector<int8_t> &rows, const float *scale, int 
   M.k = k;
   M.n = n;
   M.kp = (int)round_up(k, 64);
-  M.np = (int)round_up(n, 128);
+  M.np = (int)round_up(n, 256);
   std::vector<int8_t> q((size_t)M.np * M.kp, 0);
   std::vector<float> sb(M.np, 0.f), zc(M.np, 0.f);
   std::vector<int32_t> c128(M.np, 0);
@@ -153,11 +155,16 @@ int upload_mat(Mat &M, const std::vector<int8_t> &rows, const float *scale, int 
     zc[d] = 128.0f * (float)colsum;
     c128[d] = 128 * colsum;
   }
+  std::vector<int8_t> qk(q.size());
+  for (int d = 0; d < M.np; d++)
+    for (int t = 0; t < M.kp; t++)
+      qk[((size_t)(t / 32) * M.np + d) * 32 + t % 32] = q[(size_t)d * M.kp + t];
   int rc;
-  if ((rc = M.q.ensure(q.size())) || (rc = M.sb.ensure(sb.size() * 4)) ||
+  if ((rc = M.q.ensure(q.size())) || (rc = M.qk.ensure(qk.size())) || (rc = M.sb.ensure(sb.size() * 4)) ||
       (rc = M.zc.ensure(zc.size() * 4)) || (rc = M.c128.ensure(c128.size() * 4)))
     return rc;
   HIPCK(hipMemcpy(M.q.p, q.data(), q.size(), hipMemcpyHostToDevice));
+  HIPCK(hipMemcpy(M.qk.p, qk.data(), qk.size(), hipMemcpyHostToDevice));
   HIPCK(hipMemcpy(M.sb.p, sb.data(), sb.size() * 4, hipMemcpyHostToDevice));
   HIPCK(hipMemcpy(M.zc.p, zc.data(), zc.size() * 4, hipMemcpyHostToDevice));
   HIPCK(hipMemcpy(M.c128.p, c128.data(), c128.size() * 4, hipMemcpyHostToDevice));
@@ -439,6 +446,21 @@ struct Prof {
 
 // Streams a large batch is split over: IXH_SPLIT=1 (one pass) .. 4; default 2
 // (read at every call: tuning and tests change it between calls).
+// GEMM dispatch: the A-stationary kernel (gemm_as.hip) where it applies
+// (IXH_GEMM_AS=0 turns it off: tests and comparisons), gemm_i8 otherwise.
+// The residual epilogues stay on gemm_i8: their HBM loads would hold up
+// gemm_as's in-order weight stream.
+bool gemm_as_enabled() {
+  const char *e = getenv("IXH_GEMM_AS");
+  return !(e && e[0] == '0');
+}
+
+void run_gemm(int epi, const GemmArgs &g, hipStream_t st) {
+  const bool as_epi = epi == EPI_GEGLU || epi == EPI_STORE || epi == EPI_TILE;
+  if (as_epi && gemm_as_enabled() && launch_gemm_as(epi, g, st)) return;
+  launch_gemm(epi, g, st);
+}
+
 int split_parts() {
   const char *e = getenv("IXH_SPLIT");
   const int v = e ? atoi(e) : 2;
@@ -577,6 +599,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     g.lda = Kp;
     g.B = M.q.as<int8_t>();
     g.ldb = M.kp;
+    g.Bk = M.qk.as<int8_t>();
     g.M = N;
     g.Np = M.np;
     g.Kp = M.kp;
@@ -676,7 +699,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     RUN("ln_quant", 0, ln_bytes, launch_rownorm(ln, st));
     g = gemm(EPI_GEGLU, L.i, KpH, w->g.as<float>(), I, I);
     RUN("gemm_wi", 2 * dN * 2 * dI * dH, gemm_bytes(dH, 2 * dI, dI, false),
-        launch_gemm(EPI_GEGLU, g, st));
+        run_gemm(EPI_GEGLU, g, st));
     RUN("quant_g", 0, dN * (4 * dI + dI + 4),
         launch_quant_rows(w->g.as<float>(), I, N, I, w->xq.as<int8_t>(), KpI, w->sa.as<float>(), st));
     g = gemm(EPI_ACCUM_MLP, L.omlp, KpI, w->x.as<float>(), H, H);
@@ -1169,7 +1192,8 @@ int ixh_matmul8(ixh_packed_b8 *b, float *c, const float *a, int m, int accumulat
   g.C = dc.as<float>();
   g.ldc = M.n;
   g.n_valid = M.n;
-  launch_gemm(accumulate ? EPI_ACCUM : EPI_STORE, g, ts.s);
+  g.Bk = M.qk.as<int8_t>();
+  run_gemm(accumulate ? EPI_ACCUM : EPI_STORE, g, ts.s);
   LAUNCHCK("matmul8");
   HIPCK(hipMemcpyAsync(c, dc.p, 4 * (size_t)m * M.n, hipMemcpyDeviceToHost, ts.s));
   HIPCK(hipStreamSynchronize(ts.s));
@@ -1204,7 +1228,8 @@ int ixh_matmul8_tile(ixh_packed_b8 *b, const float *a, int m, int8_t *aq, float 
     g.Ci = dt.as<int32_t>();
     g.ldc = M.n;
     g.n_valid = M.n;
-    launch_gemm(EPI_TILE, g, ts.s);
+    g.Bk = M.qk.as<int8_t>();
+    run_gemm(EPI_TILE, g, ts.s);
     LAUNCHCK("matmul8_tile");
     HIPCK(hipMemcpyAsync(tile, dt.p, 4 * (size_t)m * M.n, hipMemcpyDeviceToHost, ts.s));
   }
@@ -1316,7 +1341,8 @@ int ixh_ln_matmul8_geglu(ixh_packed_b8 *b, const float *x, int m, const float *g
   ga.n_valid = n / 2;
   ga.lanes = lanes;
   ga.n_gelu = gelu_fma_cols(n / 2, lanes);
-  launch_gemm(EPI_GEGLU, ga, ts.s);
+  ga.Bk = M.qk.as<int8_t>();
+  run_gemm(EPI_GEGLU, ga, ts.s);
   LAUNCHCK("geglu");
   HIPCK(hipMemcpyAsync(g, dg.p, 4 * (size_t)m * (n / 2), hipMemcpyDeviceToHost, ts.s));
   if (tile) {
@@ -1325,6 +1351,7 @@ int ixh_ln_matmul8_geglu(ixh_packed_b8 *b, const float *x, int m, const float *g
     if ((rc = dt.ensure(4 * (size_t)m * n))) return rc;
     GemmArgs gt = ga;
     gt.B = N0.q.as<int8_t>();
+    gt.Bk = N0.qk.as<int8_t>();
     gt.Np = N0.np;
     gt.sb = N0.sb.as<float>();
     gt.zc = N0.zc.as<float>();
@@ -1333,7 +1360,7 @@ int ixh_ln_matmul8_geglu(ixh_packed_b8 *b, const float *x, int m, const float *g
     gt.C = nullptr;
     gt.ldc = n;
     gt.n_valid = n;
-    launch_gemm(EPI_TILE, gt, ts.s);
+    run_gemm(EPI_TILE, gt, ts.s);
     LAUNCHCK("geglu_tile");
     HIPCK(hipMemcpyAsync(tile, dt.p, 4 * (size_t)m * n, hipMemcpyDeviceToHost, ts.s));
   }

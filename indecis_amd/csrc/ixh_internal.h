@@ -24,6 +24,7 @@ struct GemmArgs {
   int lda;
   const int8_t *B;
   int ldb;
+  const int8_t *Bk;      // the same weights K-blocked [Kp/32][Np][32] (gemm_as), or nullptr
   int M, Np, Kp;
   const float *sa;       // [M]
   const float *sb;       // [Np]
@@ -50,6 +51,12 @@ struct GemmArgs {
 };
 
 void launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
+
+// The A-stationary GEMM (gemm_as.hip) for EPI_STORE/ACCUM/ACCUM_MLP/TILE/
+// GEGLU: needs Bk, Np a multiple of 256 and Kp one of 256, 512, 768, 1152;
+// returns false (nothing launched) otherwise.
+bool gemm_as_supported(const GemmArgs &a);
+bool launch_gemm_as(int epi, const GemmArgs &a, hipStream_t s);
 
 // ---- row kernels ----------------------------------------------------------
 struct RowArgs {

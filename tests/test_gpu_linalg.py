@@ -129,11 +129,13 @@ def test_attend8_exact(n, window, lanes):
     assert f32_bits_equal(o, ref), mismatch_report(o, ref)
 
 
-@pytest.mark.parametrize("tile_cfg", ["1", "2"])
+@pytest.mark.parametrize("tile_cfg", ["0", "1", "2"])
 def test_gemm_tile_configs(tile_cfg, monkeypatch):
-    """The 256x128 / 3-stage and 128x128 / 3-stage tile configurations
-    (IXH_GEMM_TILE) give the same reference tile and floats as the default,
-    on ragged shapes that leave partial M tiles and padded N and K."""
+    """The gemm_i8 kernel alone (IXH_GEMM_AS=0) in its default 128x128 and
+    its 256x128 / 3-stage and 128x128 / 3-stage tile configurations
+    (IXH_GEMM_TILE) gives the oracle's reference tile and floats, on ragged
+    shapes that leave partial M tiles and padded N and K."""
+    monkeypatch.setenv("IXH_GEMM_AS", "0")
     monkeypatch.setenv("IXH_GEMM_TILE", tile_cfg)
     rng = np.random.default_rng(int(tile_cfg))
     for m, k, n in [(7, 384, 1152), (257, 70, 40), (300, 1152, 768), (1000, 768, 2304)]:
@@ -152,6 +154,47 @@ def test_gemm_tile_configs(tile_cfg, monkeypatch):
     cfg = small_cfg()
     w = Weights.random(cfg, seed=5)
     gpu, ora = Model(w, lanes=8), orc.OracleModel(w, lanes=8)
+    seqs = ids_uniform_lengths(rng, 5, 1, 300, cfg.vocab)
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    gpu.close()
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+
+
+@pytest.mark.parametrize("kind", ["random", "max", "mixed"])
+@pytest.mark.parametrize("m,k,n", [(1, 768, 256), (63, 256, 768), (65, 512, 1000), (130, 256, 1024),
+                                   (1000, 768, 2304), (3001, 1152, 768)])
+def test_gemm_as_exact(m, k, n, kind):
+    """The A-stationary GEMM (gemm_as.hip: the default wherever K is 256,
+    512, 768 or 1152) gives the oracle's reference tile and floats, stored
+    and accumulated: partial 64-row M-blocks, N padded to 256, runs of
+    units that cross M-blocks, the largest tiles (all weights 127)."""
+    rng = np.random.default_rng(m * 13 + k + n)
+    a = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    if kind == "max":
+        a[:] = np.abs(a) + 1
+    q, s = _weights(rng, n, k, kind)
+    b = linalg.PackedB8(q, s)
+    aq, sa, tile = linalg.matmul8_tile(a, b)
+    aq_ref, sa_ref = orc.quantize_rows(a)
+    assert np.array_equal(aq, aq_ref)
+    assert np.array_equal(tile, orc.matmul8_tile(aq_ref, q))
+    colsum = q.astype(np.int32).sum(axis=1).astype(np.int32)
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    for acc in (False, True):
+        ref = orc.matmul8(a, q, s, colsum, c=c0, accumulate=acc)
+        got = linalg.matmul8(c0.copy(), a, b, m, accumulate=acc)
+        assert f32_bits_equal(got, ref), mismatch_report(got, ref)
+
+
+def test_encoder_gemm_i8_only(monkeypatch):
+    """IXH_GEMM_AS=0: the whole encoder on gemm_i8 alone (Wi + GeGLU
+    included) equals the oracle too."""
+    monkeypatch.setenv("IXH_GEMM_AS", "0")
+    cfg = small_cfg()
+    w = Weights.random(cfg, seed=9)
+    gpu, ora = Model(w, lanes=8), orc.OracleModel(w, lanes=8)
+    rng = np.random.default_rng(9)
     seqs = ids_uniform_lengths(rng, 5, 1, 300, cfg.vocab)
     got = gpu.encode_tokens(seqs)
     want, _ = ora.encode_tokens(seqs)
