@@ -269,10 +269,8 @@ bool launch_epi(const GemmArgs &a, hipStream_t s) {
 
 }  // namespace gemm_as_impl
 
-using namespace gemm_as_impl;
-
 bool gemm_as_supported(const GemmArgs &a) {
-  return a.Bk && a.Np % CHUNK == 0 &&
+  return a.Bk && a.Np % gemm_as_impl::CHUNK == 0 &&
          (a.Kp == 256 || a.Kp == 512 || a.Kp == 768 || a.Kp == 1152);
 }
 
@@ -280,11 +278,11 @@ bool launch_gemm_as(int epi, const GemmArgs &a, hipStream_t s) {
   if (a.M <= 0) return true;
   if (!gemm_as_supported(a)) return false;
   switch (epi) {
-  case EPI_STORE: return launch_epi<EPI_STORE>(a, s);
-  case EPI_ACCUM: return launch_epi<EPI_ACCUM>(a, s);
-  case EPI_ACCUM_MLP: return launch_epi<EPI_ACCUM_MLP>(a, s);
-  case EPI_TILE: return launch_epi<EPI_TILE>(a, s);
-  case EPI_GEGLU: return launch_epi<EPI_GEGLU>(a, s);
+  case EPI_STORE: return gemm_as_impl::launch_epi<EPI_STORE>(a, s);
+  case EPI_ACCUM: return gemm_as_impl::launch_epi<EPI_ACCUM>(a, s);
+  case EPI_ACCUM_MLP: return gemm_as_impl::launch_epi<EPI_ACCUM_MLP>(a, s);
+  case EPI_TILE: return gemm_as_impl::launch_epi<EPI_TILE>(a, s);
+  case EPI_GEGLU: return gemm_as_impl::launch_epi<EPI_GEGLU>(a, s);
   default: return false;
   }
 }

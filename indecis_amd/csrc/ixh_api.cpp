@@ -446,18 +446,22 @@ struct Prof {
 
 // Streams a large batch is split over: IXH_SPLIT=1 (one pass) .. 4; default 2
 // (read at every call: tuning and tests change it between calls).
-// GEMM dispatch: the A-stationary kernel (gemm_as.hip) where it applies
-// (IXH_GEMM_AS=0 turns it off: tests and comparisons), gemm_i8 otherwise.
-// The residual epilogues stay on gemm_i8: their HBM loads would hold up
-// gemm_as's in-order weight stream.
-bool gemm_as_enabled() {
-  const char *e = getenv("IXH_GEMM_AS");
-  return !(e && e[0] == '0');
+// GEMM dispatch: the A-stationary kernel (gemm_as.hip) for Wi + GeGLU and
+// the plain stores (IXH_GEMM_AS=0 turns it off), gemm_i8 for the residual
+// GEMMs Wo and WoMLP. IXH_GEMM_WS=1 runs those on the warp-specialised
+// kernel (gemm_ws.hip) instead: 2-3 us faster per launch on cfg4, but the
+// kernels around it ran slower and the whole pass lost 0.5-1 ms, so it is
+// not the default.
+bool env_is(const char *name, char v) {
+  const char *e = getenv(name);
+  return e && e[0] == v;
 }
 
 void run_gemm(int epi, const GemmArgs &g, hipStream_t st) {
   const bool as_epi = epi == EPI_GEGLU || epi == EPI_STORE || epi == EPI_TILE;
-  if (as_epi && gemm_as_enabled() && launch_gemm_as(epi, g, st)) return;
+  const bool ws_epi = epi == EPI_ACCUM || epi == EPI_ACCUM_MLP;
+  if (as_epi && !env_is("IXH_GEMM_AS", '0') && launch_gemm_as(epi, g, st)) return;
+  if (ws_epi && env_is("IXH_GEMM_WS", '1') && launch_gemm_ws(epi, g, st)) return;
   launch_gemm(epi, g, st);
 }
 
@@ -693,7 +697,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     RUN("quant_ctx", 0, dN * (4 * dH + dH + 4),
         launch_quant_rows(w->ctx.as<float>(), H, N, H, w->xq.as<int8_t>(), KpH, w->sa.as<float>(), st));
     g = gemm(EPI_ACCUM, L.o, KpH, w->x.as<float>(), H, H);
-    RUN("gemm_wo", 2 * dN * dH * dH, gemm_bytes(dH, dH, dH, true), launch_gemm(EPI_ACCUM, g, st));
+    RUN("gemm_wo", 2 * dN * dH * dH, gemm_bytes(dH, dH, dH, true), run_gemm(EPI_ACCUM, g, st));
     // mlp_norm, Wi + GeGLU, x += g . WoMLP^T (infer.go:404-424)
     ln.gamma = L.mlp_norm.as<float>();
     RUN("ln_quant", 0, ln_bytes, launch_rownorm(ln, st));
@@ -704,7 +708,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
         launch_quant_rows(w->g.as<float>(), I, N, I, w->xq.as<int8_t>(), KpI, w->sa.as<float>(), st));
     g = gemm(EPI_ACCUM_MLP, L.omlp, KpI, w->x.as<float>(), H, H);
     RUN("gemm_womlp", 2 * dN * dH * dI, gemm_bytes(dI, dH, dH, true),
-        launch_gemm(EPI_ACCUM_MLP, g, st));
+        run_gemm(EPI_ACCUM_MLP, g, st));
   }
   // final_norm (infer.go:427), then pooling or the token states
   {

@@ -57,6 +57,9 @@ void launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
 // returns false (nothing launched) otherwise.
 bool gemm_as_supported(const GemmArgs &a);
 bool launch_gemm_as(int epi, const GemmArgs &a, hipStream_t s);
+// The warp-specialised GEMM (gemm_ws.hip): same operands and conditions as
+// gemm_as; MFMA waves and epilogue waves hand blocks over through LDS.
+bool launch_gemm_ws(int epi, const GemmArgs &a, hipStream_t s);
 
 // ---- row kernels ----------------------------------------------------------
 struct RowArgs {

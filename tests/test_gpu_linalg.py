@@ -131,11 +131,12 @@ def test_attend8_exact(n, window, lanes):
 
 @pytest.mark.parametrize("tile_cfg", ["0", "1", "2"])
 def test_gemm_tile_configs(tile_cfg, monkeypatch):
-    """The gemm_i8 kernel alone (IXH_GEMM_AS=0) in its default 128x128 and
+    """The gemm_i8 kernel alone (IXH_GEMM_AS=0, IXH_GEMM_WS=0) in its default 128x128 and
     its 256x128 / 3-stage and 128x128 / 3-stage tile configurations
     (IXH_GEMM_TILE) gives the oracle's reference tile and floats, on ragged
     shapes that leave partial M tiles and padded N and K."""
     monkeypatch.setenv("IXH_GEMM_AS", "0")
+    monkeypatch.setenv("IXH_GEMM_WS", "0")
     monkeypatch.setenv("IXH_GEMM_TILE", tile_cfg)
     rng = np.random.default_rng(int(tile_cfg))
     for m, k, n in [(7, 384, 1152), (257, 70, 40), (300, 1152, 768), (1000, 768, 2304)]:
@@ -187,10 +188,13 @@ def test_gemm_as_exact(m, k, n, kind):
         assert f32_bits_equal(got, ref), mismatch_report(got, ref)
 
 
-def test_encoder_gemm_i8_only(monkeypatch):
-    """IXH_GEMM_AS=0: the whole encoder on gemm_i8 alone (Wi + GeGLU
-    included) equals the oracle too."""
-    monkeypatch.setenv("IXH_GEMM_AS", "0")
+@pytest.mark.parametrize("as_on,ws_on", [("0", "0"), ("0", "1"), ("1", "1")])
+def test_encoder_gemm_kernel_choices(as_on, ws_on, monkeypatch):
+    """IXH_GEMM_AS / IXH_GEMM_WS: the whole encoder on gemm_i8 alone (Wi +
+    GeGLU and the residual GEMMs included), or with the opt-in
+    warp-specialised kernel for the residual GEMMs, equals the oracle too."""
+    monkeypatch.setenv("IXH_GEMM_AS", as_on)
+    monkeypatch.setenv("IXH_GEMM_WS", ws_on)
     cfg = small_cfg()
     w = Weights.random(cfg, seed=9)
     gpu, ora = Model(w, lanes=8), orc.OracleModel(w, lanes=8)
@@ -200,6 +204,31 @@ def test_encoder_gemm_i8_only(monkeypatch):
     want, _ = ora.encode_tokens(seqs)
     gpu.close()
     assert f32_bits_equal(got, want), mismatch_report(got, want)
+
+
+@pytest.mark.parametrize("kind", ["random", "max"])
+@pytest.mark.parametrize("m,k,n", [(1, 768, 256), (64, 256, 256), (65, 512, 768), (700, 1152, 768),
+                                   (3001, 768, 768), (4100, 1152, 768)])
+def test_gemm_ws_accumulate_exact(m, k, n, kind, monkeypatch):
+    """The warp-specialised GEMM (gemm_ws.hip, IXH_GEMM_WS=1: MatMul8N with
+    accumulate, int8.go:89-155, as the residual GEMMs run it) adds the oracle's
+    floats to C bit for bit: partial 64-row M-blocks, one-row inputs, runs
+    of units that cross M-blocks, all weights 127. Each shape runs three
+    times on the same inputs: the MFMA and epilogue waves hand blocks over
+    through LDS, and every call must give the same bits."""
+    monkeypatch.setenv("IXH_GEMM_WS", "1")
+    rng = np.random.default_rng(m * 17 + k + 3 * n)
+    a = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    if kind == "max":
+        a[:] = np.abs(a) + 1
+    q, s = _weights(rng, n, k, kind)
+    b = linalg.PackedB8(q, s)
+    colsum = q.astype(np.int32).sum(axis=1).astype(np.int32)
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    ref = orc.matmul8(a, q, s, colsum, c=c0, accumulate=True)
+    for _ in range(3):
+        got = linalg.matmul8(c0.copy(), a, b, m, accumulate=True)
+        assert f32_bits_equal(got, ref), mismatch_report(got, ref)
 
 
 def test_exp255_shortcut_every_float():
