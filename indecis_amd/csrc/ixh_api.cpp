@@ -216,9 +216,10 @@ struct RopeTab {
 
 struct Workspace {
   hipStream_t stream = nullptr;
-  DevBuf ids, offs, padoff, pos, blocks, seqorder, x, xn, qkv, xq, sa, qq, sq, kp, ks, vt, vs,
-      ctx, g, pooled, flag;
-  PinBuf host;
+  // tabs: the pass's small host-built tables, one copy: offs [B+1], padoff
+  // [B+1], blocks [2 nblocks], sequence order [B]
+  DevBuf ids, tabs, pos, x, xn, qkv, xq, sa, qq, sq, kp, ks, vt, vs, ctx, g, pooled, flag;
+  PinBuf host, flag_host;
   std::vector<hipEvent_t> events;  // profiling: begin/end pairs, reused
   hipEvent_t order[2] = {nullptr, nullptr};  // cross-stream ordering (no timing)
   ~Workspace() {
@@ -512,9 +513,8 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   const bool fused = T <= kQkvSeqMax && !(fe && fe[0] == '0');
 
   int rc;
-  if ((rc = w->offs.ensure(4 * (B + 1))) || (rc = w->padoff.ensure(4 * (B + 1))) ||
-      (rc = w->pos.ensure(4 * (size_t)N)) || (rc = w->blocks.ensure(4 * blocks.size())) ||
-      (rc = w->seqorder.ensure(4 * (size_t)B)) ||
+  const size_t ntab = 2 * (size_t)(B + 1) + blocks.size() + B;
+  if ((rc = w->tabs.ensure(4 * ntab)) || (rc = w->pos.ensure(4 * (size_t)N)) ||
       (rc = w->x.ensure(4 * (size_t)N * H)) || (rc = w->xn.ensure(4 * (size_t)N * H)) ||
       (rc = w->qkv.ensure(4 * (size_t)N * 3 * H)) || (rc = w->xq.ensure((size_t)N * ldq)) ||
       (rc = w->sa.ensure(4 * (size_t)N)) || (rc = w->qq.ensure((size_t)N * H)) ||
@@ -524,20 +524,16 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
       (rc = w->g.ensure(4 * (size_t)N * I)))
     return rc;
 
-  // small host-built tables through pinned memory
-  const size_t small = 4 * ((B + 1) * 2 + blocks.size() + B);
-  if ((rc = w->host.ensure(small))) return rc;
+  // small host-built tables through pinned memory, one copy
+  if ((rc = w->host.ensure(4 * ntab))) return rc;
   int32_t *hs = (int32_t *)w->host.p;
-  int32_t *hs_blocks = hs + 2 * (B + 1), *hs_order = hs_blocks + blocks.size();
   memcpy(hs, offs, 4 * (B + 1));
   memcpy(hs + B + 1, padoff.data(), 4 * (B + 1));
-  if (!blocks.empty()) memcpy(hs_blocks, blocks.data(), 4 * blocks.size());
-  if (B > 0) memcpy(hs_order, order.data(), 4 * (size_t)B);
-  HIPCK(hipMemcpyAsync(w->offs.p, hs, 4 * (B + 1), hipMemcpyHostToDevice, st));
-  HIPCK(hipMemcpyAsync(w->padoff.p, hs + B + 1, 4 * (B + 1), hipMemcpyHostToDevice, st));
-  if (!blocks.empty())
-    HIPCK(hipMemcpyAsync(w->blocks.p, hs_blocks, 4 * blocks.size(), hipMemcpyHostToDevice, st));
-  if (B > 0) HIPCK(hipMemcpyAsync(w->seqorder.p, hs_order, 4 * (size_t)B, hipMemcpyHostToDevice, st));
+  if (!blocks.empty()) memcpy(hs + 2 * (B + 1), blocks.data(), 4 * blocks.size());
+  if (B > 0) memcpy(hs + 2 * (B + 1) + blocks.size(), order.data(), 4 * (size_t)B);
+  HIPCK(hipMemcpyAsync(w->tabs.p, hs, 4 * ntab, hipMemcpyHostToDevice, st));
+  const int32_t *d_offs = w->tabs.as<int32_t>(), *d_padoff = d_offs + B + 1,
+                *d_blocks = d_offs + 2 * (B + 1), *d_order = d_blocks + blocks.size();
 
   Pending local;
   Pending &pend = defer ? *defer : local;
@@ -566,14 +562,16 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   for (int b = 0; b < B; b++) {
     const double n = offs[b + 1] - offs[b];
     keys_global += n * n;
-    for (int i = 0; i < (int)n; i++)
-      keys_local += std::min((int)n, i + Wl + 1) - std::max(0, i - Wl);
+    // pairs with |i - j| <= Wl: the diagonal, then n - d pairs at each
+    // distance d = 1 .. min(Wl, n - 1) on both sides
+    const double d = n > 0 ? std::min<double>(Wl, n - 1) : 0;
+    keys_local += n + 2 * (d * n - d * (d + 1) / 2);
   }
   const double dN = N, dH = H, dI = I;
   const double row_bytes = m->emb_format == 0 ? 4 * dH : m->emb_format == 1 ? 2 * dH : dH + 4;
 
   RUN("positions", 0, 8.0 * N,
-      launch_positions(w->offs.as<int32_t>(), w->padoff.as<int32_t>(), B, w->pos.as<int32_t>(), nullptr, st));
+      launch_positions(d_offs, d_padoff, B, w->pos.as<int32_t>(), nullptr, st));
 
   // embedding gather + embeddings.norm (infer.go:361-368) -> x; layer 0's
   // QKV reads x itself (no attn_norm, infer.go:384-389): quantise it here.
@@ -581,6 +579,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   ra.M = N;
   ra.H = H;
   ra.ids = d_ids;
+  ra.vocab = c.vocab;
   ra.emb_format = m->emb_format;
   ra.emb_f32 = m->emb_table.as<float>();
   ra.emb_bf16 = m->emb_table.as<uint16_t>();
@@ -629,8 +628,8 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   aa.H = H;
   aa.nh = nh;
   aa.N = N;
-  aa.offs = w->offs.as<int32_t>();
-  aa.padoff = w->padoff.as<int32_t>();
+  aa.offs = d_offs;
+  aa.padoff = d_padoff;
   aa.B = B;
   aa.max_n = 0;
   for (int b = 0; b < B; b++) aa.max_n = std::max(aa.max_n, offs[b + 1] - offs[b]);
@@ -644,7 +643,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   aa.vs = w->vs.as<float>();
   aa.kstat = aa.vs + (size_t)B * nh * D;
   aa.Npad = Npad;
-  aa.blocks = w->blocks.as<int32_t>();
+  aa.blocks = d_blocks;
   aa.nblocks = nblocks;
   aa.ctx = w->ctx.as<float>();
 
@@ -683,7 +682,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
       // scales are its only outputs
       RUN("gemm_qkv", 2 * dN * 3 * dH * dH,
           gemm_bytes(dH, 3 * dH, 0, false) + dN * (3 * dH + 8 * nh) + 4.0 * B * dH,
-          launch_qkv_attn(g, aa, w->seqorder.as<int32_t>(), st));
+          launch_qkv_attn(g, aa, d_order, st));
     } else {
       RUN("gemm_qkv", 2 * dN * 3 * dH * dH,
           gemm_bytes(dH, 3 * dH, 2 * dH, false) + dN * (4 + dH + 4 * nh), launch_gemm(EPI_ROPE, g, st));
@@ -724,7 +723,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   }
   if (out_kind == IXH_OUT_POOLED)
     RUN("pool", 0, dN * 4 * dH + (double)B * 4 * dH,
-        launch_pool(w->xn.as<float>(), w->offs.as<int32_t>(), B, H, c.pooling == IXH_POOL_CLS, d_out, st));
+        launch_pool(w->xn.as<float>(), d_offs, B, H, c.pooling == IXH_POOL_CLS, d_out, st));
 #undef RUN
   if (defer) return prof.err;
   // tables used by queued work stay alive until the stream has run them
@@ -1072,22 +1071,29 @@ int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs, i
     HIPCK(hipMemsetAsync(d_out, 0, 4 * (size_t)B * H, st));
   if (N == 0) return IXH_OK;
   if ((rc = weights_ready(m))) return rc;
-  // ids on the device: checked by a kernel (infer.go:308-312)
-  if ((rc = w->flag.ensure(4)) || (rc = w->host.ensure(4))) return rc;
+  // ids on the device: checked by a kernel (infer.go:308-312) whose verdict
+  // is read once the pass has run — no wait before the pass. The gather
+  // clamps ids into the table, so a bad batch computes garbage that is
+  // then discarded: d_out is zeroed and the reference's error returned.
+  if ((rc = w->flag.ensure(4)) || (rc = w->flag_host.ensure(4))) return rc;
   const int big = 0x7f7f7f7f;  // the byte fill below: larger than any index
   HIPCK(hipMemsetAsync(w->flag.p, 0x7f, 4, st));
   check_ids_kernel<<<(N + 255) / 256, 256, 0, st>>>(d_ids, N, m->cfg.vocab, w->flag.as<int>());
   LAUNCHCK("check_ids");
-  HIPCK(hipMemcpyAsync(w->host.p, w->flag.p, 4, hipMemcpyDeviceToHost, st));
-  HIPCK(hipStreamSynchronize(st));
-  const int bad = *(const int *)w->host.p;
+  HIPCK(hipMemcpyAsync(w->flag_host.p, w->flag.p, 4, hipMemcpyDeviceToHost, st));
+  ExtraWs ex(m, N);
+  rc = forward_split(m, w, ex.ws.data(), (int)ex.ws.size(), st, d_ids, offs, B, out_kind, d_out);
+  HIPCK(hipStreamSynchronize(st));  // the verdict has landed (forward_split waited for it too)
+  const int bad = *(const int *)w->flag_host.p;
   if (bad != big) {
+    const size_t out_elems = out_kind == IXH_OUT_TOKENS ? (size_t)N * H : (size_t)B * H;
+    HIPCK(hipMemsetAsync(d_out, 0, 4 * out_elems, st));
     int32_t id = 0;
-    HIPCK(hipMemcpy(&id, d_ids + bad, 4, hipMemcpyDeviceToHost));
+    HIPCK(hipMemcpyAsync(&id, d_ids + bad, 4, hipMemcpyDeviceToHost, st));
+    HIPCK(hipStreamSynchronize(st));
     return fail(IXH_ERANGE, "modernbert: id %d out of vocabulary", id);
   }
-  ExtraWs ex(m, N);
-  return forward_split(m, w, ex.ws.data(), (int)ex.ws.size(), st, d_ids, offs, B, out_kind, d_out);
+  return rc;
 }
 
 int ixh_head_logits(ixh_model *m, const float *x, int T, const float *w, const float *b,

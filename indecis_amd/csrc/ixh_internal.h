@@ -67,6 +67,7 @@ struct RowArgs {
   const float *x;          // [M][H] input (unless gather)
   // gather (embedding row, internal/modernbert/infer.go:52-59)
   const int32_t *ids;
+  int vocab;               // ids are clamped into [0, vocab) (a bad batch's result is discarded)
   int emb_format;          // 0 f32, 1 bf16 (+exact rows), 2 int8 (+row scale)
   const float *emb_f32;
   const uint16_t *emb_bf16;

@@ -30,7 +30,7 @@ struct RowSrc {
       f32 = a.x + (size_t)r * a.H;
       return;
     }
-    const int id = a.ids[r];
+    const int id = min(max(a.ids[r], 0), a.vocab - 1);
     switch (a.emb_format) {
     case 1: {
       const int slot = a.exact_slot[id];
@@ -80,7 +80,7 @@ struct RowLoad {
     if constexpr (SRC == 0) {
       f = a.x + (size_t)R * a.H;
     } else {
-      const int id = a.ids[R];
+      const int id = min(max(a.ids[R], 0), a.vocab - 1);
       if constexpr (SRC == 1) {
         f = a.emb_f32 + (size_t)id * a.H;
       } else if constexpr (SRC == 2) {
