@@ -185,6 +185,21 @@ void ixh_packb8_destroy(ixh_packed_b8 *b);
 int ixh_matmul8(ixh_packed_b8 *b, float *c, const float *a, int m,
                 int accumulate);
 
+/* MatMul8Outliers (linalg/int8.go:272-349), the LLM.int8() decomposition:
+ * the input channels whose column max |a| exceeds ratio times the mean of
+ * the column maxima (the 32 largest when more) are zeroed in a copy of a,
+ * MatMul8N runs on the copy, and each such channel then adds
+ * a[i][j] * (q[col][j] * scale[col]) to c[i][col] in float32. ratio > 0.
+ * Host buffers. */
+int ixh_matmul8_outliers(ixh_packed_b8 *b, float *c, const float *a, int m,
+                         int accumulate, float ratio);
+
+/* siglip linear.apply (internal/siglip/encoder.go:36-49): dst[rows][n] =
+ * x . B through MatMul8Outliers (outliers != 0, ratio > 0) or MatMul8N,
+ * then AddTo(dst row, bias) when bias is not NULL. Host buffers. */
+int ixh_linear8(ixh_packed_b8 *b, float *dst, const float *x, int rows,
+                const float *bias, int outliers, float ratio);
+
 /* The integers MatMul8N works with, for bit-exact checks: the quantised
  * activations (signed, i.e. the reference's uint8 minus 128) aq[m][k],
  * their scales sa[m], and the reference tile (microKernel8Go,

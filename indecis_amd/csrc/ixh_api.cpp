@@ -1148,13 +1148,11 @@ void ixh_packb8_destroy(ixh_packed_b8 *b) {
 namespace {
 // Uploads a [m][k] f32 with rows padded to ld = roundup(k, 4), quantises
 // it into q [m][Kp] (zero padding) and sa [m] on stream st.
-int quantize_upload(const float *a, int m, int k, int Kp, DevBuf &da, DevBuf &dq, DevBuf &dsa,
-                    hipStream_t st) {
+// Host rows a [m][k] into da [m][round_up(k, 4)] (zero padding).
+int upload_rows(const float *a, int m, int k, DevBuf &da, hipStream_t st) {
   const int ld = (int)round_up(k, 4);
   int rc;
-  if ((rc = da.ensure(4 * (size_t)m * ld)) || (rc = dq.ensure((size_t)m * Kp)) ||
-      (rc = dsa.ensure(4 * (size_t)m)))
-    return rc;
+  if ((rc = da.ensure(4 * (size_t)m * ld))) return rc;
   if (ld == k) {
     HIPCK(hipMemcpyAsync(da.p, a, 4 * (size_t)m * k, hipMemcpyHostToDevice, st));
   } else {
@@ -1162,9 +1160,50 @@ int quantize_upload(const float *a, int m, int k, int Kp, DevBuf &da, DevBuf &dq
     HIPCK(hipMemcpy2DAsync(da.p, 4 * (size_t)ld, a, 4 * (size_t)k, 4 * (size_t)k, m,
                            hipMemcpyHostToDevice, st));
   }
+  return IXH_OK;
+}
+
+// quantizeA of device rows da [m][round_up(k, 4)] into dq [m][Kp], dsa [m].
+int quantize_dev(const DevBuf &da, int m, int k, int Kp, DevBuf &dq, DevBuf &dsa, hipStream_t st) {
+  const int ld = (int)round_up(k, 4);
+  int rc;
+  if ((rc = dq.ensure((size_t)m * Kp)) || (rc = dsa.ensure(4 * (size_t)m))) return rc;
   launch_quant_rows(da.as<float>(), ld, m, ld, dq.as<int8_t>(), Kp, dsa.as<float>(), st);
   LAUNCHCK("quant_rows");
   return IXH_OK;
+}
+
+int quantize_upload(const float *a, int m, int k, int Kp, DevBuf &da, DevBuf &dq, DevBuf &dsa,
+                    hipStream_t st) {
+  int rc;
+  if ((rc = upload_rows(a, m, k, da, st))) return rc;
+  return quantize_dev(da, m, k, Kp, dq, dsa, st);
+}
+
+// The input channels MatMul8Outliers splits off (linalg/int8.go:281-316),
+// from the column maxima of |A|: those above f32(ratio * mean), the mean a
+// float32 sum in channel order divided by k; when more than 32 qualify, a
+// selection of the first 32 places where a strictly larger maximum wins.
+constexpr int kMaxOutliers = 32;  // maxOutliers, int8.go:271
+std::vector<int> choose_outliers(const std::vector<float> &colmax, float ratio) {
+  const int k = (int)colmax.size();
+  float mean = 0.0f;
+  for (int j = 0; j < k; j++) mean += colmax[j];
+  mean /= (float)k;
+  const float thr = ratio * mean;
+  std::vector<int> out;
+  for (int j = 0; j < k; j++)
+    if (colmax[j] > thr) out.push_back(j);
+  if ((int)out.size() > kMaxOutliers) {
+    for (int i = 0; i < kMaxOutliers; i++) {
+      int best = i;
+      for (int x = i + 1; x < (int)out.size(); x++)
+        if (colmax[out[x]] > colmax[out[best]]) best = x;
+      std::swap(out[i], out[best]);
+    }
+    out.resize(kMaxOutliers);
+  }
+  return out;
 }
 
 struct TmpStream {
@@ -1208,6 +1247,104 @@ int ixh_matmul8(ixh_packed_b8 *b, float *c, const float *a, int m, int accumulat
   HIPCK(hipMemcpyAsync(c, dc.p, 4 * (size_t)m * M.n, hipMemcpyDeviceToHost, ts.s));
   HIPCK(hipStreamSynchronize(ts.s));
   return IXH_OK;
+}
+
+namespace {
+// MatMul8N, optionally with MatMul8Outliers' split (ratio > 0) and a bias
+// added after it (linear.apply): c[m][n] (+)= a . B (+ bias).
+int matmul8_split(ixh_packed_b8 *b, float *c, const float *a, int m, int accumulate, float ratio,
+                  const float *bias) {
+  DEVGUARD(b->device);
+  TmpStream ts;
+  HIPCK(hipStreamCreateWithFlags(&ts.s, hipStreamNonBlocking));
+  const Mat &M = b->mat;
+  const int k = M.k, n = M.n, ld = (int)round_up(k, 4);
+  DevBuf da, drest, dq, dsa, dc, dcm, dcols, dw, dbias;
+  int rc;
+  if ((rc = upload_rows(a, m, k, da, ts.s))) return rc;
+  std::vector<int> cols;
+  if (ratio > 0.f) {
+    if ((rc = dcm.ensure(4 * (size_t)k))) return rc;
+    HIPCK(hipMemsetAsync(dcm.p, 0, 4 * (size_t)k, ts.s));
+    launch_colmax(da.as<float>(), ld, m, k, dcm.as<unsigned>(), ts.s);
+    LAUNCHCK("colmax");
+    std::vector<float> colmax(k);
+    HIPCK(hipMemcpyAsync(colmax.data(), dcm.p, 4 * (size_t)k, hipMemcpyDeviceToHost, ts.s));
+    HIPCK(hipStreamSynchronize(ts.s));
+    cols = choose_outliers(colmax, ratio);
+  }
+  const int nc = (int)cols.size();
+  if (nc > 0) {
+    // the product runs on a copy of A without the chosen channels
+    if ((rc = drest.ensure(4 * (size_t)m * ld)) || (rc = dcols.ensure(4 * (size_t)nc))) return rc;
+    HIPCK(hipMemcpyAsync(drest.p, da.p, 4 * (size_t)m * ld, hipMemcpyDeviceToDevice, ts.s));
+    HIPCK(hipMemcpyAsync(dcols.p, cols.data(), 4 * (size_t)nc, hipMemcpyHostToDevice, ts.s));
+    launch_zero_cols(drest.as<float>(), ld, m, dcols.as<int>(), nc, ts.s);
+    LAUNCHCK("zero_cols");
+    if ((rc = quantize_dev(drest, m, k, M.kp, dq, dsa, ts.s))) return rc;
+  } else if ((rc = quantize_dev(da, m, k, M.kp, dq, dsa, ts.s))) {
+    return rc;
+  }
+  if ((rc = dc.ensure(4 * (size_t)m * n))) return rc;
+  if (accumulate) HIPCK(hipMemcpyAsync(dc.p, c, 4 * (size_t)m * n, hipMemcpyHostToDevice, ts.s));
+  GemmArgs g{};
+  g.A = dq.as<int8_t>();
+  g.lda = M.kp;
+  g.B = M.q.as<int8_t>();
+  g.ldb = M.kp;
+  g.M = m;
+  g.Np = M.np;
+  g.Kp = M.kp;
+  g.sa = dsa.as<float>();
+  g.sb = M.sb.as<float>();
+  g.zc = M.zc.as<float>();
+  g.c128 = M.c128.as<int32_t>();
+  g.C = dc.as<float>();
+  g.ldc = n;
+  g.n_valid = n;
+  g.Bk = M.qk.as<int8_t>();
+  run_gemm(accumulate ? EPI_ACCUM : EPI_STORE, g, ts.s);
+  LAUNCHCK("matmul8");
+  std::vector<float> w;
+  if (nc > 0 || bias) {
+    // the split channels' dequantised weight rows: f32(q) * scale (int8.go:336-340)
+    w.resize((size_t)std::max(nc, 1) * n);
+    for (int t = 0; t < nc; t++)
+      for (int col = 0; col < n; col++)
+        w[(size_t)t * n + col] = (float)b->rows[(size_t)col * k + cols[t]] * b->scale[col];
+    if ((rc = dw.ensure(4 * w.size()))) return rc;
+    HIPCK(hipMemcpyAsync(dw.p, w.data(), 4 * w.size(), hipMemcpyHostToDevice, ts.s));
+    if (bias) {
+      if ((rc = dbias.ensure(4 * (size_t)n))) return rc;
+      HIPCK(hipMemcpyAsync(dbias.p, bias, 4 * (size_t)n, hipMemcpyHostToDevice, ts.s));
+    }
+    launch_outlier_epilogue(dc.as<float>(), n, m, n, da.as<float>(), ld, nc ? dcols.as<int>() : nullptr, nc,
+                            dw.as<float>(), bias ? dbias.as<float>() : nullptr, ts.s);
+    LAUNCHCK("outlier_epilogue");
+  }
+  HIPCK(hipMemcpyAsync(c, dc.p, 4 * (size_t)m * n, hipMemcpyDeviceToHost, ts.s));
+  HIPCK(hipStreamSynchronize(ts.s));  // w and cols outlive their copies
+  return IXH_OK;
+}
+
+}  // namespace
+
+int ixh_matmul8_outliers(ixh_packed_b8 *b, float *c, const float *a, int m, int accumulate,
+                         float ratio) {
+  if (!b || m < 0 || (m > 0 && (!c || !a)))
+    return fail(IXH_EINVAL, "linalg: MatMul8Outliers: slice too short");
+  if (m == 0 || b->mat.n == 0) return IXH_OK;
+  if (!(ratio > 0.f)) return fail(IXH_EINVAL, "linalg: MatMul8Outliers: ratio %g", (double)ratio);
+  return matmul8_split(b, c, a, m, accumulate, ratio, nullptr);
+}
+
+int ixh_linear8(ixh_packed_b8 *b, float *dst, const float *x, int rows, const float *bias,
+                int outliers, float ratio) {
+  if (!b || rows < 0 || (rows > 0 && (!dst || !x)))
+    return fail(IXH_EINVAL, "siglip: linear: slice too short");
+  if (rows == 0) return IXH_OK;
+  if (outliers && !(ratio > 0.f)) return fail(IXH_EINVAL, "siglip: linear: ratio %g", (double)ratio);
+  return matmul8_split(b, dst, x, rows, 0, outliers ? ratio : 0.f, bias);
 }
 
 int ixh_matmul8_tile(ixh_packed_b8 *b, const float *a, int m, int8_t *aq, float *sa,

@@ -61,6 +61,15 @@ bool launch_gemm_as(int epi, const GemmArgs &a, hipStream_t s);
 // gemm_as; MFMA waves and epilogue waves hand blocks over through LDS.
 bool launch_gemm_ws(int epi, const GemmArgs &a, hipStream_t s);
 
+// ---- MatMul8Outliers / linear.apply (outliers.hip) --------------------------
+// out[j] |= bits of max_i |a[i][j]| (out zeroed first)
+void launch_colmax(const float *a, int ld, int m, int k, unsigned *out, hipStream_t s);
+// a[i][cols[t]] = 0
+void launch_zero_cols(float *a, int ld, int m, const int *cols, int ncols, hipStream_t s);
+// c[i][col] = (c + a[i][cols[0]] * w[0][col] + ...) + bias[col] (bias may be null)
+void launch_outlier_epilogue(float *c, int ldc, int m, int n, const float *a, int lda, const int *cols,
+                             int ncols, const float *w, const float *bias, hipStream_t s);
+
 // ---- row kernels ----------------------------------------------------------
 struct RowArgs {
   int M, H;

@@ -53,6 +53,35 @@ def matmul8(c, a, b, m, accumulate=False):
     return c
 
 
+def matmul8_outliers(c, a, b, m, accumulate=False, ratio=6.0):
+    """MatMul8Outliers (int8.go:272-349): c[m][n] (+)= a[m][k] . B with the
+    LLM.int8() split of massive input channels, in place."""
+    if c.dtype != np.float32 or not c.flags.c_contiguous:
+        raise ValueError("linalg: MatMul8Outliers: c must be contiguous float32")
+    if a.size < m * b.k or c.size < m * b.n:
+        raise ValueError("linalg: MatMul8Outliers: slice too short")
+    a = np.ascontiguousarray(a, np.float32)
+    _lib.check(_lib.lib().ixh_matmul8_outliers(b._h, _ptr(c), _ptr(a), m, 1 if accumulate else 0,
+                                               float(ratio)))
+    return c
+
+
+def linear8(x, b, bias=None, outliers=False, ratio=6.0):
+    """siglip linear.apply (encoder.go:36-49): x[rows][k] . B (+ bias)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows = x.shape[0]
+    if x.shape[1] != b.k:
+        raise ValueError("siglip: linear: slice too short")
+    dst = np.zeros((rows, b.n), np.float32)
+    bias_c = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    if bias_c is not None and bias_c.size < b.n:
+        raise ValueError("siglip: linear: bias too short")
+    _lib.check(_lib.lib().ixh_linear8(b._h, _ptr(dst), _ptr(x), rows,
+                                      None if bias_c is None else _ptr(bias_c),
+                                      1 if outliers else 0, float(ratio)))
+    return dst
+
+
 def matmul8_tile(a, b):
     """The integers of MatMul8N: (aq signed [m][k], sa [m], tile [m][n])
     with tile = sum (aq+128)*q as microKernel8Go computes it."""

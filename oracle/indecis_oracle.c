@@ -218,6 +218,85 @@ void ixo_matmul8(float *c, int ldc, const float *a, int lda, const int8_t *w,
   free(sa);
 }
 
+/* linalg/int8.go:272-349. */
+int ixo_matmul8_outliers(float *c, int ldc, const float *a, int lda, const int8_t *w,
+                         const float *sb, const int32_t *colsum, int m, int k, int n,
+                         int accumulate, float ratio, int *cols) {
+  if (m == 0 || n == 0) return 0;
+  /* column maxima of |a| (abs32 clears the sign bit, int8.go:203) */
+  float *colmax = (float *)calloc((size_t)k + 1, sizeof(float));
+  for (int i = 0; i < m; i++)
+    for (int j = 0; j < k; j++) {
+      const float v = fabsf(a[(size_t)i * lda + j]);
+      colmax[j] = fmax32(colmax[j], v);
+    }
+  float mean = 0.0f; /* float32, in channel order (int8.go:289-293) */
+  for (int j = 0; j < k; j++) mean += colmax[j];
+  mean /= (float)k;
+  const float thr = ratio * mean;
+  int *out = (int *)malloc(sizeof(int) * ((size_t)k + 1));
+  int nout = 0;
+  for (int j = 0; j < k; j++)
+    if (colmax[j] > thr) out[nout++] = j;
+  if (nout == 0) {
+    free(colmax);
+    free(out);
+    ixo_matmul8(c, ldc, a, lda, w, sb, colsum, m, k, n, accumulate);
+    return 0;
+  }
+  if (nout > 32) {
+    /* keep the largest: selection of the first 32 places, a strictly larger
+     * maximum wins (int8.go:304-316) */
+    for (int i = 0; i < 32; i++) {
+      int best = i;
+      for (int x = i + 1; x < nout; x++)
+        if (colmax[out[x]] > colmax[out[best]]) best = x;
+      const int t = out[i];
+      out[i] = out[best];
+      out[best] = t;
+    }
+    nout = 32;
+  }
+  float *rest = (float *)malloc(sizeof(float) * ((size_t)m * k + 1));
+  for (int i = 0; i < m; i++) {
+    memcpy(rest + (size_t)i * k, a + (size_t)i * lda, sizeof(float) * (size_t)k);
+    for (int t = 0; t < nout; t++) rest[(size_t)i * k + out[t]] = 0.0f;
+  }
+  ixo_matmul8(c, ldc, rest, k, w, sb, colsum, m, k, n, accumulate);
+  float *wd = (float *)malloc(sizeof(float) * ((size_t)n + 1));
+  for (int t = 0; t < nout; t++) {
+    const int j = out[t];
+    for (int col = 0; col < n; col++) wd[col] = (float)w[(size_t)col * k + j] * sb[col];
+    for (int i = 0; i < m; i++) {
+      const float x = a[(size_t)i * lda + j];
+      float *ci = c + (size_t)i * ldc;
+      for (int col = 0; col < n; col++) {
+        const float p = x * wd[col]; /* separate rounding: no FMA (gc, amd64) */
+        ci[col] = ci[col] + p;
+      }
+    }
+    if (cols) cols[t] = j;
+  }
+  free(wd);
+  free(rest);
+  free(colmax);
+  free(out);
+  return nout;
+}
+
+/* internal/siglip/encoder.go:36-49. */
+void ixo_linear8(float *dst, const float *x, const int8_t *w, const float *sb,
+                 const int32_t *colsum, int rows, int k, int n, const float *bias,
+                 int outliers, float ratio) {
+  if (outliers)
+    ixo_matmul8_outliers(dst, n, x, k, w, sb, colsum, rows, k, n, 0, ratio, NULL);
+  else
+    ixo_matmul8(dst, n, x, k, w, sb, colsum, rows, k, n, 0);
+  if (bias)
+    for (int r = 0; r < rows; r++)
+      for (int col = 0; col < n; col++) dst[(size_t)r * n + col] = dst[(size_t)r * n + col] + bias[col];
+}
+
 /* linalg/vec_simd.go:285-327 (lanes V > 0): float32 lane partials of the
  * sum, added in float64; float32 lane partials of fma(d, d, sq); float64
  * tail. lanes == 0: vec_scalar.go:66-81. */

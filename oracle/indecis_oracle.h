@@ -69,6 +69,23 @@ void ixo_matmul8(float *c, int ldc, const float *a, int lda, const int8_t *w,
                  const float *sb, const int32_t *colsum, int m, int k, int n,
                  int accumulate);
 
+/* MatMul8Outliers (linalg/int8.go:272-349): the input channels whose
+ * column max |a| exceeds f32(ratio * mean of the column maxima) — the 32
+ * largest when more — are zeroed in a copy of a, MatMul8N runs on the
+ * copy, then each such channel j (in the chosen order) adds
+ * a[i][j] * f32(w[col][j] * sb[col]) to c[i][col]. Writes the chosen
+ * channels to cols (room for 32) and returns their number. */
+int ixo_matmul8_outliers(float *c, int ldc, const float *a, int lda, const int8_t *w,
+                         const float *sb, const int32_t *colsum, int m, int k, int n,
+                         int accumulate, float ratio, int *cols);
+
+/* linear.apply (internal/siglip/encoder.go:36-49): MatMul8Outliers (ratio)
+ * or MatMul8N (outliers == 0) into dst, then AddTo(dst row, bias) when
+ * bias is not NULL (vec_scalar.go:97-101). */
+void ixo_linear8(float *dst, const float *x, const int8_t *w, const float *sb,
+                 const int32_t *colsum, int rows, int k, int n, const float *bias,
+                 int outliers, float ratio);
+
 /* LayerNormRow (linalg/vec_simd.go:285-327; lanes==0: vec_scalar.go:66-81). */
 void ixo_layernorm_row(float *o, const float *x, const float *gamma, int n,
                        double eps, int lanes);

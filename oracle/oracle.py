@@ -69,6 +69,11 @@ def lib():
                                       C.c_int, C.c_int, C.c_int, C.c_int]
         L.ixo_matmul8.argtypes = [f32p, C.c_int, f32p, C.c_int, i8p, f32p, i32p,
                                   C.c_int, C.c_int, C.c_int, C.c_int]
+        L.ixo_matmul8_outliers.argtypes = [f32p, C.c_int, f32p, C.c_int, i8p, f32p, i32p, C.c_int,
+                                           C.c_int, C.c_int, C.c_int, C.c_float, i32p]
+        L.ixo_matmul8_outliers.restype = C.c_int
+        L.ixo_linear8.argtypes = [f32p, f32p, i8p, f32p, i32p, C.c_int, C.c_int, C.c_int,
+                                  C.c_void_p, C.c_int, C.c_float]
         L.ixo_layernorm_row.argtypes = [f32p, f32p, f32p, C.c_int, C.c_double, C.c_int]
         L.ixo_gelu_mul.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int]
         L.ixo_exp_shift.argtypes = [f32p, C.c_int, C.c_float, C.c_int]
@@ -163,6 +168,33 @@ def matmul8(a, wq, sb, colsum, c=None, accumulate=False):
         lib().ixo_matmul8(out, n, a, k, _c(wq, np.int8), _c(sb, np.float32),
                           _c(colsum, np.int32), m, k, n, 1 if accumulate else 0)
     return out
+
+
+def matmul8_outliers(a, wq, sb, colsum, ratio, c=None, accumulate=False):
+    """MatMul8Outliers (linalg/int8.go:272-349): (c, chosen input channels)."""
+    a = _c(a, np.float32)
+    m, k = a.shape
+    n = wq.shape[0]
+    out = np.zeros((m, n), np.float32) if c is None else _c(c, np.float32).copy()
+    cols = np.zeros(32, np.int32)
+    nout = lib().ixo_matmul8_outliers(out, n, a, k, _c(wq, np.int8), _c(sb, np.float32),
+                                      _c(colsum, np.int32), m, k, n, 1 if accumulate else 0,
+                                      float(ratio), cols)
+    return out, cols[:nout].copy()
+
+
+def linear8(x, wq, sb, colsum, bias=None, outliers=False, ratio=6.0):
+    """siglip linear.apply (encoder.go:36-49): x . W^T (+ bias)."""
+    x = _c(x, np.float32)
+    rows, k = x.shape
+    n = wq.shape[0]
+    dst = np.zeros((rows, n), np.float32)
+    if rows:
+        keep = _c(bias, np.float32) if bias is not None else None  # alive during the call
+        bptr = keep.ctypes.data if keep is not None else None
+        lib().ixo_linear8(dst, x, _c(wq, np.int8), _c(sb, np.float32), _c(colsum, np.int32), rows, k, n,
+                          bptr, 1 if outliers else 0, float(ratio))
+    return dst
 
 
 def matmul8_deq(q, sa, wq, sb, colsum, c=None, accumulate=False):

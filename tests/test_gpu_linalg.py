@@ -231,6 +231,70 @@ def test_gemm_ws_accumulate_exact(m, k, n, kind, monkeypatch):
         assert f32_bits_equal(got, ref), mismatch_report(got, ref)
 
 
+def _outlier_inputs(case, rng):
+    if case == "reference":  # TestMatMul8Outliers (int8_test.go:98-118)
+        m, k, n = 64, 3072, 96
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        a[:, 1038] = 1000 * rng.standard_normal(m).astype(np.float32)
+        a[:, 7] = 150
+        b = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+        q, s, cs = orc.pack_b8(b, k, n, transB=False)
+        return a, q, s, cs
+    m, k, n = {"many": (33, 1000, 300), "ties": (9, 1000, 40), "none": (70, 768, 256),
+               "large": (3000, 768, 768), "one_row": (1, 1152, 768)}[case]
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    if case == "many":
+        for j in rng.choice(k, 45, replace=False):
+            a[:, j] *= float(rng.uniform(400, 2000))
+    elif case == "ties":
+        for j in range(40):
+            a[:, 3 * j] = 5000.0 * np.sign(a[:, 3 * j] + 1e-3)
+        a[0, [1, 4, 7, 10, 13]] = [8000, 7000, 8000, 6000, 7500]
+    elif case in ("large", "one_row"):
+        a[:, [5, 300, 700]] *= 250
+    q, s, cs = orc.pack_b8(rng.standard_normal((n, k)).astype(np.float32), k, n)
+    return a, q, s, cs
+
+
+@pytest.mark.parametrize("case", ["reference", "many", "ties", "none", "large", "one_row"])
+def test_matmul8_outliers_exact(case):
+    """MatMul8Outliers on the GPU (column maxima, the host's channel choice,
+    the int8 product of the zeroed copy, the float32 adds of the split
+    channels) equals the oracle bit for bit, stored and accumulated; with
+    no channel over the bar it is MatMul8N's result."""
+    rng = np.random.default_rng(["reference", "many", "ties", "none", "large", "one_row"].index(case) + 3)
+    a, q, s, cs = _outlier_inputs(case, rng)
+    m, n = a.shape[0], q.shape[0]
+    b = linalg.PackedB8(q, s)
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    for acc in (False, True):
+        want, cols = orc.matmul8_outliers(a, q, s, cs, 6.0, c=c0, accumulate=acc)
+        got = linalg.matmul8_outliers(c0.copy(), a, b, m, accumulate=acc, ratio=6.0)
+        assert f32_bits_equal(got, want), mismatch_report(got, want)
+    if case == "none":
+        assert len(cols) == 0
+        plain = linalg.matmul8(c0.copy(), a, b, m, accumulate=True)
+        assert f32_bits_equal(got, plain)
+    elif case in ("many", "ties"):
+        assert len(cols) == 32
+
+
+@pytest.mark.parametrize("outliers", [False, True])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_linear8_exact(outliers, with_bias):
+    """siglip linear.apply (encoder.go:36-49) on the GPU: the product (split
+    or not), then the bias, equal to the oracle bit for bit."""
+    rng = np.random.default_rng(10 + outliers + 2 * with_bias)
+    rows, k, n = 729, 768, 3072  # SigLIP-base fc1 over one image's 27x27 patches
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x[:, [11, 400]] *= 300
+    q, s, cs = orc.pack_b8(rng.standard_normal((n, k)).astype(np.float32), k, n)
+    bias = rng.standard_normal(n).astype(np.float32) if with_bias else None
+    want = orc.linear8(x, q, s, cs, bias, outliers, 6.0)
+    got = linalg.linear8(x, linalg.PackedB8(q, s), bias, outliers, 6.0)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+
+
 def test_exp255_shortcut_every_float():
     """The attention kernels round 255*exp(v) from the hardware exponential
     and fall back to the reference formulas (ExpShift's vector body and

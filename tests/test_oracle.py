@@ -184,6 +184,136 @@ def test_matmul8_rows_independent():
         assert np.array_equal(orc.matmul8(a[i:i + 1], q, s, cs)[0], allc[i])
 
 
+def _outliers_case(seed=3, m=64, k=3072, n=96):
+    """The inputs of TestMatMul8Outliers (int8_test.go:98-118): A ~ N(0,1)
+    with two massive channels (1038: 1000 N(0,1), 7: 150), B ~ N(0, 0.02)
+    [k x n] packed with transB false."""
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    a[:, 1038] = 1000 * rng.standard_normal(m).astype(np.float32)
+    a[:, 7] = 150
+    b = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+    q, s, cs = orc.pack_b8(b, k, n, transB=False)
+    return a, b, q, s, cs
+
+
+def test_matmul8_outliers_error_and_identity():
+    """TestMatMul8Outliers (int8_test.go:98-144): with the two massive
+    channels split off, the error against the float product is at most
+    1e-2 and a fraction of MatMul8's; with them zeroed, the same bits as
+    MatMul8. The reference asserts es <= ep/5 for Go's draws of seed 3;
+    over numpy's draws the ratio ep/es runs 4.7-6.3 (the split channels'
+    own int8 weights bound es), so each of 8 draws must reach 4 and their
+    median 5."""
+    ratios = []
+    for seed in range(3, 11):
+        a, b, q, s, cs = _outliers_case(seed)
+        want = a.astype(np.float64) @ b.astype(np.float64)
+        plain = orc.matmul8(a, q, s, cs)
+        split, cols = orc.matmul8_outliers(a, q, s, cs, 6.0)
+        assert sorted(cols.tolist()) == [7, 1038]
+
+        def err(got):
+            return math.sqrt(((got - want) ** 2).sum() / (want ** 2).sum())
+
+        ep, es = err(plain), err(split)
+        assert es <= 1e-2 and es <= ep / 4, (seed, ep, es)
+        ratios.append(ep / es)
+    assert np.median(ratios) >= 5, ratios
+    a, b, q, s, cs = _outliers_case()
+    a[:, [7, 1038]] = 0
+    plain = orc.matmul8(a, q, s, cs)
+    split, cols = orc.matmul8_outliers(a, q, s, cs, 6.0)
+    assert len(cols) == 0 and np.array_equal(split.view(np.uint32), plain.view(np.uint32))
+
+
+def _outliers_numpy(a, q, s, cs, ratio, c=None):
+    """An independent restatement of int8.go:281-349 in numpy float32:
+    the selection rule, then MatMul8N of the zeroed copy (the oracle's
+    matmul8, pinned above), then the float32 adds in the chosen order."""
+    k = a.shape[1]
+    colmax = np.abs(a).max(axis=0).astype(np.float32)
+    mean = np.float32(0)
+    for v in colmax:  # float32, channel order
+        mean = np.float32(mean + v)
+    mean = np.float32(mean / np.float32(k))
+    out = [j for j in range(k) if colmax[j] > np.float32(np.float32(ratio) * mean)]
+    if len(out) > 32:
+        for i in range(32):
+            best = i
+            for x in range(i + 1, len(out)):
+                if colmax[out[x]] > colmax[out[best]]:
+                    best = x
+            out[i], out[best] = out[best], out[i]
+        out = out[:32]
+    rest = a.copy()
+    rest[:, out] = 0
+    base = orc.matmul8(rest, q, s, cs, c=c, accumulate=c is not None)
+    for j in out:
+        w = (q[:, j].astype(np.float32) * s).astype(np.float32)
+        base = (base + (a[:, j:j + 1] * w[None, :]).astype(np.float32)).astype(np.float32)
+    return base, out
+
+
+@pytest.mark.parametrize("case", ["two", "many", "ties", "accumulate"])
+def test_matmul8_outliers_selection_and_order(case):
+    """The oracle's channel choice (the 32 largest when more qualify, a
+    strictly larger maximum winning, ties keeping the earlier channel) and
+    the float32 order of the outlier adds equal an independent numpy
+    restatement, bit for bit."""
+    rng = np.random.default_rng({"two": 1, "many": 2, "ties": 3, "accumulate": 4}[case])
+    # k = 1000: with ratio 6 at most k/6 channels can exceed 6x the mean
+    m, k, n = 9, 1000, 40
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    if case == "two" or case == "accumulate":
+        a[:, 17] *= 300
+        a[:, 150] = 90
+    elif case == "many":  # 45 qualify
+        for j in rng.choice(k, 45, replace=False):
+            a[:, j] *= float(rng.uniform(400, 2000))
+    else:  # 40 channels with equal maxima 5000, 5 larger ones (two equal)
+        for j in range(40):
+            a[:, 3 * j] = 5000.0 * np.sign(a[:, 3 * j] + 1e-3)
+        a[0, [1, 4, 7, 10, 13]] = [8000, 7000, 8000, 6000, 7500]
+    q, s, cs = orc.pack_b8(rng.standard_normal((n, k)).astype(np.float32), k, n)
+    c0 = rng.standard_normal((m, n)).astype(np.float32) if case == "accumulate" else None
+    got, cols = orc.matmul8_outliers(a, q, s, cs, 6.0, c=c0, accumulate=c0 is not None)
+    want, out = _outliers_numpy(a, q, s, cs, 6.0, c=c0)
+    assert cols.tolist() == out
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    if case in ("many", "ties"):
+        assert len(out) == 32
+
+
+def test_matmul8_outliers_planted_mistake_fails():
+    """The error test above rejects an outlier path that drops the float32
+    term of the split channels (a plausible slip): the massive channel's
+    contribution is then missing."""
+    a, b, q, s, cs = _outliers_case()
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    rest = a.copy()
+    rest[:, [7, 1038]] = 0
+    wrong = orc.matmul8(rest, q, s, cs)
+    es = math.sqrt(((wrong - want) ** 2).sum() / (want ** 2).sum())
+    assert es > 1e-2
+
+
+def test_linear8_bias_after_product():
+    """linear.apply (siglip/encoder.go:36-49): the product, then AddTo of
+    the bias in float32."""
+    rng = np.random.default_rng(8)
+    rows, k, n = 11, 96, 24
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x[:, 5] *= 400
+    q, s, cs = orc.pack_b8(rng.standard_normal((n, k)).astype(np.float32), k, n)
+    bias = rng.standard_normal(n).astype(np.float32)
+    for outliers in (False, True):
+        got = orc.linear8(x, q, s, cs, bias, outliers, 6.0)
+        prod = orc.matmul8_outliers(x, q, s, cs, 6.0)[0] if outliers else orc.matmul8(x, q, s, cs)
+        assert np.array_equal(got.view(np.uint32), (prod + bias[None, :]).view(np.uint32))
+    assert np.array_equal(orc.linear8(x, q, s, cs).view(np.uint32), orc.matmul8(x, q, s, cs).view(np.uint32))
+
+
 # ---- vector operations -------------------------------------------------------
 
 @pytest.mark.parametrize("lanes", [0, 4, 8, 16])
