@@ -33,6 +33,7 @@ enum {
   IXH_ESTATE = 3,   /* weights missing (infer.go:170-182) */
   IXH_EHIP = 4,     /* HIP runtime error ("modernbert: hip: ...") */
   IXH_ENOMEM = 5,
+  IXH_EFORMAT = 6,  /* unreadable or malformed weights file (safetensors.go:112-224) */
 };
 
 /* modernbert.Config (internal/modernbert/model.go:26-49) plus the Go simd
@@ -98,6 +99,24 @@ int ixh_model_set_embeddings_bf16(ixh_model *m, const uint16_t *table,
                                   const float *exact_rows, int n_exact);
 int ixh_model_set_embeddings_i8(ixh_model *m, const int8_t *table,
                                 const float *row_scale);
+
+/* Every weight of the model from an indecis model.safetensors (Load,
+ * model.go:640-740; FromTensors names, internal/modernbert/model.go:
+ * 181-234, "model." prefix accepted): the embedding table uploaded in its
+ * stored format (I8 + "indecis.embeddings.scale", BF16 + the exact rows,
+ * or F32/F16 decoded), each layer matrix decoded (F32, BF16, F16, I8) and
+ * packed by PackB8 (linalg/int8.go:38-77) on the host one at a time, the
+ * LayerNorm weights decoded. The file is memory-mapped and checked as
+ * safetensors.Parse checks it (IXH_EFORMAT and its message otherwise);
+ * shapes must match the handle's config. */
+int ixh_model_load_safetensors(ixh_model *m, const char *path);
+
+/* safetensors.File.Tensor (safetensors.go:160-173): tensor `name` of the
+ * file decoded to float32 (BF16 and F16 widened, I8 as integers) into out
+ * (room for cap floats); *count receives its element count (out may be
+ * NULL to ask only for it). Host only: no GPU is touched. */
+int ixh_safetensors_tensor(const char *path, const char *name, float *out,
+                           int64_t cap, int64_t *count);
 
 /* Optional: RoPE tables as Go's ropeFor computes them (model.go:256-277),
  * cos/sin [rows][head_dim/2], for the global (is_global=1) or local theta.

@@ -18,14 +18,14 @@ EXPORTS = [
     "ixh_model_set_embeddings_bf16", "ixh_model_set_embeddings_i8", "ixh_model_set_rope",
     "ixh_model_invalidate", "ixh_encode_seqs", "ixh_encode_tokens", "ixh_encode_device",
     "ixh_head_logits", "ixh_packb8_create", "ixh_packb8_destroy", "ixh_matmul8",
-    "ixh_matmul8_outliers", "ixh_linear8",
+    "ixh_matmul8_outliers", "ixh_linear8", "ixh_model_load_safetensors", "ixh_safetensors_tensor",
     "ixh_matmul8_tile", "ixh_layernorm_quant", "ixh_ln_matmul8_geglu", "ixh_attend8",
     "ixh_model_set_profiling", "ixh_model_set_profile_filter", "ixh_model_profile",
     "ixh_check_exp255", "ixh_batcher_create", "ixh_batcher_encode", "ixh_batcher_stats",
     "ixh_batcher_destroy",
 ]
 
-IXH_OK, IXH_EINVAL, IXH_ERANGE, IXH_ESTATE, IXH_EHIP, IXH_ENOMEM = range(6)
+IXH_OK, IXH_EINVAL, IXH_ERANGE, IXH_ESTATE, IXH_EHIP, IXH_ENOMEM, IXH_EFORMAT = range(7)
 POOL_MEAN, POOL_CLS = 0, 1
 MAT_QKV, MAT_O, MAT_I, MAT_OMLP = range(4)
 NORM_EMB, NORM_ATTN, NORM_MLP, NORM_FINAL = range(4)
@@ -87,6 +87,8 @@ def lib():
         "ixh_packb8_create": [C.c_int, vp, vp, C.c_int, C.c_int, C.c_int, C.POINTER(vp)],
         "ixh_matmul8": [vp, vp, vp, C.c_int, C.c_int],
         "ixh_matmul8_outliers": [vp, vp, vp, C.c_int, C.c_int, C.c_float],
+        "ixh_model_load_safetensors": [vp, C.c_char_p],
+        "ixh_safetensors_tensor": [C.c_char_p, C.c_char_p, vp, C.c_int64, C.POINTER(C.c_int64)],
         "ixh_linear8": [vp, vp, vp, C.c_int, vp, C.c_int, C.c_float],
         "ixh_matmul8_tile": [vp, vp, C.c_int, vp, vp, vp],
         "ixh_layernorm_quant": [C.c_int, vp, C.c_int, C.c_int, vp, C.c_double, C.c_int, vp, vp, vp],

@@ -850,6 +850,14 @@ int encode_host(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, in
 
 }  // namespace
 
+namespace ixh {
+int set_error(int code, const char *msg) {
+  g_err = msg;
+  return code;
+}
+void model_config(const ixh_model *m, ixh_config *out) { *out = m->cfg; }
+}  // namespace ixh
+
 // ==== C ABI =================================================================
 extern "C" {
 

@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+struct ixh_model;   // include/indecis_hip.h
+struct ixh_config;
+
 namespace ixh {
 
 // ---- int8 GEMM ----------------------------------------------------------
@@ -60,6 +63,12 @@ bool launch_gemm_as(int epi, const GemmArgs &a, hipStream_t s);
 // The warp-specialised GEMM (gemm_ws.hip): same operands and conditions as
 // gemm_as; MFMA waves and epilogue waves hand blocks over through LDS.
 bool launch_gemm_ws(int epi, const GemmArgs &a, hipStream_t s);
+
+// ---- host helpers (ixh_api.cpp) ---------------------------------------------
+// Sets the calling thread's ixh_last_error message; returns code.
+int set_error(int code, const char *msg);
+// The config a model handle was created with.
+void model_config(const ::ixh_model *m, ::ixh_config *out);
 
 // ---- MatMul8Outliers / linear.apply (outliers.hip) --------------------------
 // out[j] |= bits of max_i |a[i][j]| (out zeroed first)

@@ -185,8 +185,8 @@ def _offsets(seqs):
 class Model:
     """modernbert.Model on the int8 path, its weights resident on one GPU."""
 
-    def __init__(self, weights, device=0, lanes=8):
-        self.cfg = cfg = weights.cfg
+    def __init__(self, weights, device=0, lanes=8, cfg=None):
+        self.cfg = cfg = weights.cfg if weights is not None else cfg
         cfg.validate()
         self.lanes = lanes
         L = _lib.lib()
@@ -201,7 +201,26 @@ class Model:
         self._h = h
         self._L = L
         self.device = device
-        self.upload(weights)
+        if weights is not None:
+            self.upload(weights)
+
+    @classmethod
+    def open(cls, cfg, path, device=0, lanes=8):
+        """Load (model.go:640-740) of an indecis model.safetensors straight
+        into device memory: see load_safetensors."""
+        m = cls(None, device=device, lanes=lanes, cfg=cfg)
+        try:
+            m.load_safetensors(path)
+        except Exception:
+            m.close()
+            raise
+        return m
+
+    def load_safetensors(self, path):
+        """Every weight from a model.safetensors (ixh_model_load_safetensors):
+        the embedding table in its stored format, each layer matrix packed
+        by PackB8 on the host, the LayerNorm weights."""
+        _lib.check(self._L.ixh_model_load_safetensors(self._h, str(path).encode()))
 
     def upload(self, w):
         """packs() (infer.go:184-219): uploads every matrix and table."""
