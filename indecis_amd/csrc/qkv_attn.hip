@@ -70,20 +70,33 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
   // its chunk: row i/4, physical 16-byte column i%4 (logical (i%4) ^ swz).
   const int lrow = lane >> 2, lchunk = (lane & 3) ^ swz(lane >> 2);
   const int nchunk = 2 * nbc + 4;
+  // This wave's chunks q = wave + 8c (c < nch <= 5, wave-uniform): the
+  // source of each lane and the LDS offset in a stage, computed once; a K
+  // step then only adds kt * BK.
+  constexpr int MAXCH = (2 * (SEQ_MAX / 32) + 4 + 7) / 8;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int nch = wave_u < nchunk ? (nchunk - wave_u + 7) / 8 : 0;
+  const int8_t *csrc[MAXCH];
+  int cdst[MAXCH];
+#pragma unroll
+  for (int c = 0; c < MAXCH; c++) {
+    const int q = wave_u + 8 * c;
+    if (q < 2 * nbc) {
+      const int row = min(16 * q + lrow, n - 1);
+      csrc[c] = g.A + (size_t)(base + row) * g.lda + 16 * lchunk;
+      cdst[c] = 16 * q * BK;
+    } else {
+      const int qb = min(q - 2 * nbc, 3);  // c >= nch: never issued
+      csrc[c] = g.B + (size_t)(col0 + 16 * qb + lrow) * g.ldb + 16 * lchunk;
+      cdst[c] = A_BYTES + 16 * qb * BK;
+    }
+  }
   auto issue = [&](int kt) {
     int8_t *st = smem + (kt & 1) * STAGE;
-    const int k0 = kt * BK + 16 * lchunk;
-    for (int q = wave; q < nchunk; q += 8) {
-      if (q < 2 * nbc) {
-        const int row = min(16 * q + lrow, n - 1);
-        __builtin_amdgcn_global_load_lds((glb_ptr)(g.A + (size_t)(base + row) * g.lda + k0),
-                                         (lds_ptr)(st + 16 * q * BK), 16, 0, 0);
-      } else {
-        const int qb = q - 2 * nbc;
-        __builtin_amdgcn_global_load_lds((glb_ptr)(g.B + (size_t)(col0 + 16 * qb + lrow) * g.ldb + k0),
-                                         (lds_ptr)(st + A_BYTES + 16 * qb * BK), 16, 0, 0);
-      }
-    }
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++)
+      if (c < nch)
+        __builtin_amdgcn_global_load_lds((glb_ptr)(csrc[c] + kt * BK), (lds_ptr)(st + cdst[c]), 16, 0, 0);
   };
 
   v16i acc[2][2];
@@ -113,8 +126,8 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
       }
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        if (wave + 8 * i < nbc) {
-          const int row = 32 * (wave + 8 * i) + fr;
+        if (wave_u + 8 * i < nbc) {
+          const int row = 32 * (wave_u + 8 * i) + fr;
           const v4i fa = *(const v4i *)(st + row * BK + 16 * ((2 * s + fh) ^ swz(row)));
 #pragma unroll
           for (int j = 0; j < 2; j++) acc[i][j] = mfma32(fa, fb[j], acc[i][j]);
