@@ -118,6 +118,46 @@ int ixh_model_load_safetensors(ixh_model *m, const char *path);
 int ixh_safetensors_tensor(const char *path, const char *name, float *out,
                            int64_t cap, int64_t *count);
 
+/* ---- tokenizer (host only: no GPU is touched) --------------------------- */
+
+/* The Gemma-family BPE tokenizer of tokenizer/tokenizer.go (exact parity
+ * with Hugging Face tokenizers for the configurations it accepts). Load
+ * (tokenizer.go:80-94, the tokenizer.json path; configurations the
+ * reference rejects are rejected with its messages, IXH_EFORMAT). The
+ * handle is immutable: any number of threads may encode with it. */
+typedef struct ixh_tokenizer ixh_tokenizer;
+int ixh_tokenizer_load(const char *path, ixh_tokenizer **out);
+void ixh_tokenizer_destroy(ixh_tokenizer *t);
+/* VocabSize, BosID, EosID, PadID (tokenizer.go:443-461); any may be NULL. */
+int ixh_tokenizer_info(const ixh_tokenizer *t, int32_t *vocab_size,
+                       int32_t *bos, int32_t *eos, int32_t *pad);
+/* Encode (max_len < 0) or EncodeMax (tokenizer.go:479-495) of text[len]
+ * (UTF-8, invalid bytes as Go reads them): *n ids, written to ids when it
+ * is not NULL (room for cap). */
+int ixh_tokenizer_encode(const ixh_tokenizer *t, const char *text,
+                         int64_t len, int max_len, int32_t *ids, int64_t cap,
+                         int64_t *n);
+/* EncodePair (tokenizer.go:497-518): the pair template, max_len > 0
+ * truncating the context before the text (0: no limit, as there). */
+int ixh_tokenizer_encode_pair(const ixh_tokenizer *t, const char *context,
+                              int64_t clen, const char *text, int64_t tlen,
+                              int max_len, int32_t *ids, int64_t cap,
+                              int64_t *n);
+/* EncodeOffsets (tokenizer.go:525-540): ids and the byte span
+ * [starts[i], ends[i]) of each in text (template specials: [0, 0)). */
+int ixh_tokenizer_encode_offsets(const ixh_tokenizer *t, const char *text,
+                                 int64_t len, int32_t *ids, int64_t *starts,
+                                 int64_t *ends, int64_t cap, int64_t *n);
+/* No reference counterpart (the reference tokenizes one text per call,
+ * model.go:202-210): EncodeMax of n texts on `threads` threads (0: one per
+ * core; max_len < 0: Encode), laid end to end in ids (room for cap) with
+ * offs[n+1] cumulative —
+ * the ids/offs of ixh_encode_seqs. With ids NULL only offs is filled. */
+int ixh_tokenizer_encode_batch(const ixh_tokenizer *t,
+                               const char *const *texts, const int64_t *lens,
+                               int n, int max_len, int threads, int32_t *ids,
+                               int64_t cap, int32_t *offs);
+
 /* Optional: RoPE tables as Go's ropeFor computes them (model.go:256-277),
  * cos/sin [rows][head_dim/2], for the global (is_global=1) or local theta.
  * Without them the library computes the same formula with the C library's

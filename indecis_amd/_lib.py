@@ -19,6 +19,8 @@ EXPORTS = [
     "ixh_model_invalidate", "ixh_encode_seqs", "ixh_encode_tokens", "ixh_encode_device",
     "ixh_head_logits", "ixh_packb8_create", "ixh_packb8_destroy", "ixh_matmul8",
     "ixh_matmul8_outliers", "ixh_linear8", "ixh_model_load_safetensors", "ixh_safetensors_tensor",
+    "ixh_tokenizer_load", "ixh_tokenizer_destroy", "ixh_tokenizer_info", "ixh_tokenizer_encode",
+    "ixh_tokenizer_encode_pair", "ixh_tokenizer_encode_offsets", "ixh_tokenizer_encode_batch",
     "ixh_matmul8_tile", "ixh_layernorm_quant", "ixh_ln_matmul8_geglu", "ixh_attend8",
     "ixh_model_set_profiling", "ixh_model_set_profile_filter", "ixh_model_profile",
     "ixh_check_exp255", "ixh_batcher_create", "ixh_batcher_encode", "ixh_batcher_stats",
@@ -88,6 +90,13 @@ def lib():
         "ixh_matmul8": [vp, vp, vp, C.c_int, C.c_int],
         "ixh_matmul8_outliers": [vp, vp, vp, C.c_int, C.c_int, C.c_float],
         "ixh_model_load_safetensors": [vp, C.c_char_p],
+        "ixh_tokenizer_load": [C.c_char_p, C.POINTER(vp)],
+        "ixh_tokenizer_info": [vp, vp, vp, vp, vp],
+        "ixh_tokenizer_encode": [vp, C.c_char_p, C.c_int64, C.c_int, vp, C.c_int64, C.POINTER(C.c_int64)],
+        "ixh_tokenizer_encode_pair": [vp, C.c_char_p, C.c_int64, C.c_char_p, C.c_int64, C.c_int, vp, C.c_int64,
+                                      C.POINTER(C.c_int64)],
+        "ixh_tokenizer_encode_offsets": [vp, C.c_char_p, C.c_int64, vp, vp, vp, C.c_int64, C.POINTER(C.c_int64)],
+        "ixh_tokenizer_encode_batch": [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int64, vp],
         "ixh_safetensors_tensor": [C.c_char_p, C.c_char_p, vp, C.c_int64, C.POINTER(C.c_int64)],
         "ixh_linear8": [vp, vp, vp, C.c_int, vp, C.c_int, C.c_float],
         "ixh_matmul8_tile": [vp, vp, C.c_int, vp, vp, vp],
@@ -113,6 +122,8 @@ def lib():
     L.ixh_packb8_destroy.restype = None
     L.ixh_batcher_destroy.argtypes = [vp]
     L.ixh_batcher_destroy.restype = None
+    L.ixh_tokenizer_destroy.argtypes = [vp]
+    L.ixh_tokenizer_destroy.restype = None
     _lib = L
     return L
 
