@@ -132,6 +132,89 @@ def serving(np, model, cfg, args):
     }), flush=True)
 
 
+def tokenize(np, args):
+    """Host tokenizer throughput (tokenizer.go's EncodeMax on many texts):
+    ixh_tokenizer_encode_batch on the box's CPU share, beside Hugging Face
+    tokenizers (the library whose output the reference reproduces) on the
+    same texts and threads, ids checked equal; then text to pooled rows on
+    the GPU for one batch, tokenizer included. Texts: documents of
+    U[256, 2048] bytes built from the texts of the reference's siglip2-tiny
+    fixtures (multilingual, emoji, code), on its tokenizer.json."""
+    gold = os.path.join(ROOT, "tests", "golden", "tokenizer")
+    pool = [json.loads(line)["text"] for line in open(os.path.join(gold, "tokenizer_cases.jsonl"), encoding="utf-8")]
+    pool = [t for t in pool if t]
+    rng = np.random.default_rng(11)
+    docs = []
+    for _ in range(args.docs):
+        want, parts, n = int(rng.integers(256, 2049)), [], 0
+        while n < want:
+            t = pool[int(rng.integers(len(pool)))]
+            parts.append(t)
+            n += len(t.encode("utf-8")) + 1
+        docs.append(" ".join(parts))
+    nbytes = sum(len(d.encode("utf-8")) for d in docs)
+    threads = min(16, os.cpu_count() or 1)
+    os.environ.setdefault("RAYON_NUM_THREADS", str(threads))
+    from indecis_amd.tokenizer import Tokenizer
+    path = os.path.join(gold, "tokenizer.json")
+    tok = Tokenizer(path)
+
+    def rate(fn, reps):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            r = fn()
+        return (time.perf_counter() - t0) / reps, r
+
+    native = {}
+    for th in (1, threads):
+        dt, (ids, offs) = rate(lambda: tok.encode_batch(docs, threads=th), args.steps)
+        native[th] = dt
+    ntok = int(offs[-1])
+    hf = None
+    try:
+        from tokenizers import Tokenizer as HF
+    except ImportError:
+        HF = None
+    if HF is not None:
+        h = HF.from_file(path)
+        dt, enc = rate(lambda: h.encode_batch(docs), max(1, args.steps // 2))
+        same = all(e.ids == ids[offs[i]:offs[i + 1]].tolist() for i, e in enumerate(enc))
+        hf = {"value": round(ntok / dt, 1), "unit": "tokens/s", "threads": threads, "ids_equal": same,
+              "kind": "tokenizers (Rust), encode_batch"}
+    e2e = None
+    import torch
+    if torch.cuda.is_available():
+        from indecis_amd.modernbert import BASE, Model, Weights
+        model = Model(Weights.random(BASE, seed=4), device=0, lanes=args.lanes)
+        batch = docs[:256]
+
+        def text_to_rows():
+            i, o = tok.encode_batch(batch, max_len=512, threads=threads)
+            return model.encode_seqs([i[o[k]:o[k + 1]] for k in range(len(batch))])
+        bi, bo = tok.encode_batch(batch, max_len=512, threads=threads)
+        seqs = [bi[bo[k]:bo[k + 1]] for k in range(len(batch))]
+        t_all, _ = rate(text_to_rows, args.steps)
+        t_enc, _ = rate(lambda: model.encode_seqs(seqs), args.steps)
+        model.close()
+        e2e = {"texts": len(batch), "tokens": int(bo[-1]), "ms_text_to_rows": round(t_all * 1e3, 3),
+               "ms_ids_to_rows": round(t_enc * 1e3, 3),
+               "note": "EncodeMax(512) of 256 documents on the host, then EncodeSeqs (host ids in, pooled rows "
+                       "out) on the GPU, ModernBERT-base shape"}
+    print(json.dumps({
+        "metric": "host tokenizer tokens/s (EncodeMax over a batch of documents)",
+        "value": round(ntok / native[threads], 1), "unit": "tokens/s", "higher_is_better": True,
+        "threads": threads, "data": "synthetic",
+        "config": {"workload": f"{len(docs)} documents of U[256,2048] bytes from the siglip2-tiny fixture texts",
+                   "tokenizer": "siglip2-tiny tokenizer.json (raw Gemma pipeline, 3,252 ids)",
+                   "bytes": nbytes, "tokens": ntok},
+        "single_thread": {"value": round(ntok / native[1], 1), "MB_per_s": round(nbytes / native[1] / 1e6, 2)},
+        "MB_per_s": round(nbytes / native[threads] / 1e6, 2),
+        "hf_tokenizers": hf,
+        "text_to_rows": e2e,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -149,6 +232,9 @@ def main():
                     help="instead: concurrent single-sequence requests, direct calls vs the batcher")
     ap.add_argument("--clients", type=int, default=32)
     ap.add_argument("--requests", type=int, default=40, help="requests per client (--serving)")
+    ap.add_argument("--tokenize", action="store_true",
+                    help="instead: host tokenizer throughput, and text to pooled rows for one batch")
+    ap.add_argument("--docs", type=int, default=4096, help="documents (--tokenize)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -157,6 +243,9 @@ def main():
         sys.exit(2)
 
     import numpy as np
+    if args.tokenize:
+        tokenize(np, args)
+        return
     import torch
 
     from indecis_amd import _lib

@@ -152,7 +152,8 @@ int ixh_tokenizer_encode_offsets(const ixh_tokenizer *t, const char *text,
  * model.go:202-210): EncodeMax of n texts on `threads` threads (0: one per
  * core; max_len < 0: Encode), laid end to end in ids (room for cap) with
  * offs[n+1] cumulative —
- * the ids/offs of ixh_encode_seqs. With ids NULL only offs is filled. */
+ * the ids/offs of ixh_encode_seqs. With ids NULL, or cap below the total,
+ * only offs is filled (the latter returns IXH_EINVAL). */
 int ixh_tokenizer_encode_batch(const ixh_tokenizer *t,
                                const char *const *texts, const int64_t *lens,
                                int n, int max_len, int threads, int32_t *ids,

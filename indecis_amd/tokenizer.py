@@ -76,9 +76,19 @@ class Tokenizer:
         offs = np.zeros(n + 1, np.int32)
         L = _lib.lib()
         p = lambda a: a.ctypes.data_as(C.c_void_p)
-        _lib.check(L.ixh_tokenizer_encode_batch(self._h, C.cast(arr, C.c_void_p), p(lens), n, max_len, threads,
-                                                None, 0, p(offs)))
-        ids = np.zeros(int(offs[-1]), np.int32)
-        _lib.check(L.ixh_tokenizer_encode_batch(self._h, C.cast(arr, C.c_void_p), p(lens), n, max_len, threads,
-                                                p(ids), ids.size, p(offs)))
-        return ids, offs
+        # One pass into room for the most a text can give: 3 ids per byte
+        # (a byte fallback of ' ' -> U+2581), 3 for a leading U+2581, and the
+        # template's specials; a second pass only if the template holds more
+        # than 16 of them.
+        bound = 3 * lens[:n] + 3 + 16
+        if max_len >= 0:
+            bound = np.minimum(bound, max(max_len, 16))
+        ids = np.empty(int(bound.sum()), np.int32)
+        rc = L.ixh_tokenizer_encode_batch(self._h, C.cast(arr, C.c_void_p), p(lens), n, max_len, threads,
+                                          p(ids), ids.size, p(offs))
+        if rc == _lib.IXH_EINVAL and n and offs[-1] > ids.size:
+            ids = np.empty(int(offs[-1]), np.int32)
+            rc = L.ixh_tokenizer_encode_batch(self._h, C.cast(arr, C.c_void_p), p(lens), n, max_len, threads,
+                                              p(ids), ids.size, p(offs))
+        _lib.check(rc)
+        return ids[:offs[-1]], offs
