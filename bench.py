@@ -183,8 +183,15 @@ def tokenize(np, args):
         hf = {"value": round(ntok / dt, 1), "unit": "tokens/s", "threads": threads, "ids_equal": same,
               "kind": "tokenizers (Rust), encode_batch"}
     e2e = None
-    import torch
-    if torch.cuda.is_available():
+    # No torch here: with this library loaded before torch (the tokenizer
+    # loads it), its HIP runtime found no device once torch had initialised
+    # its own; the other modes import torch before loading the library.
+    from indecis_amd import _lib
+    try:
+        gpus = _lib.device_count()
+    except _lib.IxhError:
+        gpus = 0
+    if gpus:
         from indecis_amd.modernbert import BASE, Model, Weights
         model = Model(Weights.random(BASE, seed=4), device=0, lanes=args.lanes)
         batch = docs[:256]
