@@ -16,13 +16,18 @@
 // The outputs are those of the QKV GEMM (EPI_ROPE, queries) plus
 // launch_attn_prologue: qq, sq, kp, ks, vt, vs, same layouts, same bits.
 //
-// Layout: 8 waves; 32-row block rb of the sequence (rb < 16) belongs to
-// wave rb % 8, which holds it as 2 MFMA 32x32 tiles (the head's 64
-// columns). K steps of 64 stream A (the sequence's rows, up to 32 KB) and
-// B (the head's 64 weight rows, 4 KB) into a 2-stage LDS ring with
-// direct-to-LDS loads, as the GEMM does. Workgroups are dealt so that the
-// 36 of a sequence (12 heads x Q, K, V) run on one XCD and share its rows
-// in L2; sequences go longest first, spread over the 8 XCDs.
+// Layout: NH halves of 8 waves, half f computing head NH*hp + f; in a
+// half, 32-row block rb of the sequence (rb < 16) belongs to wave rb % 8,
+// which holds it as 2 MFMA 32x32 tiles (the head's 64 columns). K steps of
+// 64 stream A (the sequence's rows, up to 32 KB) and B (the NH heads' 64
+// weight rows each, 4 KB a head) into an LDS ring with direct-to-LDS
+// loads, as the GEMM does; every wave of the workgroup issues a share of
+// the chunks. NH = 1: 512 threads, a 2-stage ring, two workgroups a CU.
+// NH = 2: 1,024 threads, a 3-stage ring (two stages in flight), one
+// workgroup a CU: each A row brought into LDS feeds two heads, so the
+// sequence's rows are read 18 times instead of 36. Workgroups are dealt so
+// that those of a sequence (12 heads x Q, K, V) run on one XCD and share
+// its rows in L2; sequences go longest first, spread over the 8 XCDs.
 #include "ixh_device.h"
 #include "ixh_internal.h"
 
@@ -33,66 +38,92 @@ namespace {
 constexpr int D = 64, BK = 64, NXCD = 8;
 constexpr int SEQ_MAX = kQkvSeqMax;           // 512 rows
 constexpr int A_BYTES = SEQ_MAX * BK;         // A part of a stage
-constexpr int STAGE = A_BYTES + D * BK;       // + B part
 constexpr int KT_LD = 68;                     // floats per row of the Q/K slab
 constexpr int SLAB_BYTES = 256 * KT_LD * 4;   // 256 keys
-constexpr int SMEM = 2 * STAGE > SLAB_BYTES ? 2 * STAGE : SLAB_BYTES;
 constexpr int VT_LD = 48;                     // bytes per dimension of the V^T staging tile
 
-__global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a, const int32_t *order) {
+constexpr int cmax(int x, int y) { return x > y ? x : y; }
+template <int NH>
+struct Shape {
+  static constexpr int NW = 8 * NH;                     // waves
+  static constexpr int RING = NH == 1 ? 2 : 3;          // stages
+  static constexpr int STAGE = A_BYTES + NH * D * BK;   // A + the heads' B rows
+  // dynamic LDS: the ring, else one slab a half, the RoPE tables (8 KB a
+  // wave) or the V^T tiles
+  static constexpr int SMEM = cmax(cmax(RING * STAGE, NH * SLAB_BYTES), cmax(NW * 8192, NW * D * VT_LD));
+};
+
+// s_waitcnt vmcnt(n) for a wave-uniform n <= 3 (an immediate each).
+__device__ __forceinline__ void wait_vmcnt_upto(int n) {
+  if (n <= 0) wait_vmcnt<0>();
+  else if (n == 1) wait_vmcnt<1>();
+  else if (n == 2) wait_vmcnt<2>();
+  else wait_vmcnt<3>();
+}
+
+template <int NH>
+__global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a, const int32_t *order) {
+  using S = Shape<NH>;
+  constexpr int NW = S::NW, RING = S::RING, STAGE = S::STAGE;
   extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
   __shared__ float sa_s[SEQ_MAX];
-  __shared__ float red_s[8][D];
-  __shared__ __attribute__((aligned(16))) float stat_s[D];
+  __shared__ float red_s[NH][8][D];
+  __shared__ __attribute__((aligned(16))) float stat_s[NH][D];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hf = wave >> 3, wv = wave & 7, tidh = tid & 511;  // half, wave and thread in the half
   const int fr = lane & 31, fh = lane >> 5;
-  const int per_seq = 3 * a.nh;
+  const int hgroups = a.nh / NH;
+  const int per_seq = 3 * hgroups;
   const int xcd = blockIdx.x % NXCD, k = blockIdx.x / NXCD;
   const int si = xcd + NXCD * (k / per_seq);
   if (si >= a.B) return;
   const int b = order[si];
-  const int part = (k % per_seq) / a.nh, h = (k % per_seq) % a.nh;
+  const int part = (k % per_seq) / hgroups, h0 = NH * ((k % per_seq) % hgroups), h = h0 + hf;
   const int base = a.offs[b], n = a.offs[b + 1] - base;
   const int npad = (n + kKeyPad - 1) / kKeyPad * kKeyPad;
   const int nb = npad / 32;            // 32-row blocks stored (even, at most 16)
   const int nbc = (n + 31) / 32;       // blocks computed: a block past n is all zeros
-  const int col0 = part * a.H + h * D;  // the head's first output column
+  const int col0 = part * a.H + h * D;   // this half's head: first output column
+  const int colb = part * a.H + h0 * D;  // the workgroup's first weight row
   if (n == 0) {
-    if (part == 2 && tid < D) a.vs[((size_t)b * a.nh + h) * D + tid] = 0.f;
+    if (part == 2 && tidh < D) a.vs[((size_t)b * a.nh + h) * D + tidh] = 0.f;
     return;
   }
-  for (int t = tid; t < 32 * nb; t += 512) sa_s[t] = g.sa[base + min(t, n - 1)];
+  for (int t = tid; t < 32 * nb; t += 512 * NH) sa_s[t] = g.sa[base + min(t, n - 1)];
 
   // ---- int8 GEMM of the sequence's rows by the head's 64 weight rows ----
   // Stage chunks of 16 rows x 64 bytes (one wave instruction each): A
   // chunks 0 .. 2nbc-1 (rows past n load row n-1, never stored), then the
-  // 4 B chunks; chunk q is loaded by wave q % 8. Lane i fills 16 bytes of
-  // its chunk: row i/4, physical 16-byte column i%4 (logical (i%4) ^ swz).
+  // 4 NH B chunks (head f's at A_BYTES + f * 64 rows); chunk q is loaded by
+  // wave q % NW. Lane i fills 16 bytes of its chunk: row i/4, physical
+  // 16-byte column i%4 (logical (i%4) ^ swz).
   const int lrow = lane >> 2, lchunk = (lane & 3) ^ swz(lane >> 2);
-  const int nchunk = 2 * nbc + 4;
-  // This wave's chunks q = wave + 8c (c < nch <= 5, wave-uniform): the
-  // source of each lane and the LDS offset in a stage, computed once; a K
-  // step then only adds kt * BK.
-  constexpr int MAXCH = (2 * (SEQ_MAX / 32) + 4 + 7) / 8;
+  const int nchunk = 2 * nbc + 4 * NH;
+  // This wave's chunks q = wave + NW c (c < nch <= MAXCH, wave-uniform):
+  // the source of each lane and the LDS offset in a stage, computed once;
+  // a K step then only adds kt * BK.
+  constexpr int MAXCH = (2 * (SEQ_MAX / 32) + 4 * NH + NW - 1) / NW;
+  static_assert(MAXCH <= 3 || RING == 2, "wait_vmcnt_upto covers 3 chunks a stage");
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const int nch = wave_u < nchunk ? (nchunk - wave_u + 7) / 8 : 0;
+  const int wv_u = wave_u & 7;
+  const int nch = wave_u < nchunk ? (nchunk - wave_u + NW - 1) / NW : 0;
   const int8_t *csrc[MAXCH];
   int cdst[MAXCH];
 #pragma unroll
   for (int c = 0; c < MAXCH; c++) {
-    const int q = wave_u + 8 * c;
+    const int q = wave_u + NW * c;
     if (q < 2 * nbc) {
       const int row = min(16 * q + lrow, n - 1);
       csrc[c] = g.A + (size_t)(base + row) * g.lda + 16 * lchunk;
       cdst[c] = 16 * q * BK;
     } else {
-      const int qb = min(q - 2 * nbc, 3);  // c >= nch: never issued
-      csrc[c] = g.B + (size_t)(col0 + 16 * qb + lrow) * g.ldb + 16 * lchunk;
+      const int qb = min(q - 2 * nbc, 4 * NH - 1);  // c >= nch: never issued
+      csrc[c] = g.B + (size_t)(colb + 16 * qb + lrow) * g.ldb + 16 * lchunk;
       cdst[c] = A_BYTES + 16 * qb * BK;
     }
   }
   auto issue = [&](int kt) {
-    int8_t *st = smem + (kt & 1) * STAGE;
+    int8_t *st = smem + (kt % RING) * STAGE;
 #pragma unroll
     for (int c = 0; c < MAXCH; c++)
       if (c < nch)
@@ -109,25 +140,28 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
 
   const int nk = g.Kp / BK;
   issue(0);
+  if (RING > 2 && nk > 1) issue(1);
   for (int kt = 0; kt < nk; kt++) {
-    // this step's loads landed (nothing else is in flight), every wave's
-    // too after the barrier; the other stage is free
-    wait_vmcnt<0>();
+    // this step's loads landed (loads retire in order: at most the next
+    // stage's nch are still in flight), every wave's too after the
+    // barrier, which also ends every wave's reads of the stage issued next
+    if (RING > 2 && kt + 1 < nk) wait_vmcnt_upto(nch);
+    else wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
-    if (kt + 1 < nk) issue(kt + 1);
-    const int8_t *st = smem + (kt & 1) * STAGE;
+    if (kt + RING - 1 < nk) issue(kt + RING - 1);
+    const int8_t *st = smem + (kt % RING) * STAGE;
 #pragma unroll
     for (int s = 0; s < 2; s++) {
       v4i fb[2];
 #pragma unroll
       for (int j = 0; j < 2; j++) {
-        const int row = 32 * j + fr;
+        const int row = 64 * hf + 32 * j + fr;
         fb[j] = *(const v4i *)(st + A_BYTES + row * BK + 16 * ((2 * s + fh) ^ swz(row)));
       }
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        if (wave_u + 8 * i < nbc) {
-          const int row = 32 * (wave_u + 8 * i) + fr;
+        if (wv_u + 8 * i < nbc) {
+          const int row = 32 * (wv_u + 8 * i) + fr;
           const v4i fa = *(const v4i *)(st + row * BK + 16 * ((2 * s + fh) ^ swz(row)));
 #pragma unroll
           for (int j = 0; j < 2; j++) acc[i][j] = mfma32(fa, fb[j], acc[i][j]);
@@ -151,7 +185,7 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
   float v[2][2][16];
 #pragma unroll
   for (int i = 0; i < 2; i++) {
-    if (wave + 8 * i >= nb) continue;
+    if (wv + 8 * i >= nb) continue;
     // RoPE tables (cos, sin: 32 floats a position) of the block's 32 rows,
     // staged into this wave's 8 KB of the free ring by 8 direct-to-LDS
     // loads; a row's position is its index in the sequence (padding rows:
@@ -160,7 +194,7 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
     if (part < 2) {
 #pragma unroll
       for (int u = 0; u < 4; u++) {
-        const int p = min(32 * (wave + 8 * i) + 8 * u + (lane >> 3), n - 1);
+        const int p = min(32 * (wv + 8 * i) + 8 * u + (lane >> 3), n - 1);
         const size_t off = (size_t)p * 32 + 4 * (lane & 7);
         __builtin_amdgcn_global_load_lds((glb_ptr)(g.rope_cos + off), (lds_ptr)(smem + wave * 8192 + 1024 * u), 16, 0, 0);
         __builtin_amdgcn_global_load_lds((glb_ptr)(g.rope_sin + off),
@@ -170,7 +204,7 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
     }
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const int row = 32 * (wave + 8 * i) + acc_row(r, lane);
+      const int row = 32 * (wv + 8 * i) + acc_row(r, lane);
       const float sa = sa_s[row];
       float v0 = deq(acc[i][0][r] + c128[0], zc[0], sb[0], sa);
       float v1 = deq(acc[i][1][r] + c128[1], zc[1], sb[1], sa);
@@ -192,10 +226,10 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
     float vm[2] = {0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-      if (wave + 8 * i >= nb) continue;
+      if (wv + 8 * i >= nb) continue;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        if (32 * (wave + 8 * i) + acc_row(r, lane) < n) {
+        if (32 * (wv + 8 * i) + acc_row(r, lane) < n) {
           vm[0] = fmax32(vm[0], fabsf(v[i][0][r]));
           vm[1] = fmax32(vm[1], fabsf(v[i][1][r]));
         }
@@ -204,27 +238,27 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       vm[j] = fmax32(vm[j], __shfl_xor(vm[j], 32));
-      if (fh == 0) red_s[wave][32 * j + fr] = vm[j];
+      if (fh == 0) red_s[hf][wv][32 * j + fr] = vm[j];
     }
     __syncthreads();
-    if (tid < D) {
+    if (tidh < D) {
       float vs = 0.f;
-      for (int w = 0; w < 8; w++) vs = fmax32(vs, red_s[w][tid]);
+      for (int w = 0; w < 8; w++) vs = fmax32(vs, red_s[hf][w][tidh]);
       float vi = 0.f;
       if (vs > 0.f) {  // attention8.go:262-269
         vs = vs / 127.0f;
         vi = 1.0f / vs;
       }
-      a.vs[((size_t)b * a.nh + h) * D + tid] = vs;
-      stat_s[tid] = vi;
+      a.vs[((size_t)b * a.nh + h) * D + tidh] = vs;
+      stat_s[hf][tidh] = vi;
     }
     __syncthreads();
-    const float vi0 = stat_s[fr], vi1 = stat_s[32 + fr];
+    const float vi0 = stat_s[hf][fr], vi1 = stat_s[hf][32 + fr];
     int8_t *vt_s = smem + wave * (D * VT_LD);  // [64 dims][32 keys] of this wave's block
     int8_t *vt = a.vt + (size_t)h * D * a.Npad + a.padoff[b];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-      const int rb = wave + 8 * i;
+      const int rb = wv + 8 * i;
       if (rb < nb) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
@@ -256,11 +290,11 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
   // ---- Q and K: rows through an LDS slab of 256 rows ----
   // PUT(t): this wave's block of round t (rows 256t + 32 wave ..) into the
   // slab, in the MFMA layout
-  float *slab = (float *)smem;  // [256 rows][KT_LD]
+  float *slab = (float *)(smem + hf * SLAB_BYTES);  // [256 rows][KT_LD], one a half
 #define PUT(t)                                                    \
-  if (wave + 8 * (t) < nb) {                                      \
+  if (wv + 8 * (t) < nb) {                                        \
     _Pragma("unroll") for (int r = 0; r < 16; r++) {              \
-      const int lr = 32 * wave + acc_row(r, lane);                \
+      const int lr = 32 * wv + acc_row(r, lane);                  \
       slab[lr * KT_LD + fr] = v[t][0][r];                         \
       slab[lr * KT_LD + 32 + fr] = v[t][1][r];                    \
     }                                                             \
@@ -274,14 +308,14 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
       if (256 * t < n) {  // block-uniform
         PUT(t)
         __syncthreads();
-        if (wave == 0) {
+        if (wv == 0) {
           const int cnt = min(256, n - 256 * t);
           for (int lr = 0; lr < cnt; lr++) ksum = ksum + slab[lr * KT_LD + lane];
         }
         __syncthreads();
       }
     }
-    if (wave == 0) stat_s[lane] = ksum * (1.0f / (float)n);  // Scale(mean, 1/n)
+    if (wv == 0) stat_s[hf][lane] = ksum * (1.0f / (float)n);  // Scale(mean, 1/n)
     __syncthreads();
   }
 
@@ -293,11 +327,11 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
   int8_t *kp = a.kp + ((size_t)h * a.Npad + a.padoff[b]) * D;
   float *ks = a.ks + (size_t)h * a.Npad + a.padoff[b];
   const int hh = (lane >> 4) & 1;
-  const int lr = 32 * wave + 16 * (lane >> 5) + (lane & 15);
+  const int lr = 32 * wv + 16 * (lane >> 5) + (lane & 15);
   auto quant_round = [&](int t) {
     const int row = 256 * t + lr;
     const float4 *src = (const float4 *)(slab + lr * KT_LD + 32 * hh);
-    const float4 *mu = (const float4 *)(stat_s + 32 * hh);
+    const float4 *mu = (const float4 *)(stat_s[hf] + 32 * hh);
     // the slab is read twice (max, then quantisation): fewer live registers
     auto value = [&](int c) {
       float4 x = src[c];
@@ -369,15 +403,45 @@ __global__ __launch_bounds__(512, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a
 
 }  // namespace
 
+namespace {
+
+// hipFuncSetAttribute once per variant: 1 set, -1 refused (that variant is
+// then not used), 0 not tried yet.
+template <int NH>
+bool smem_ready() {
+  static int state = 0;
+  if (state == 0)
+    state = hipFuncSetAttribute((const void *)qkv_attn_kernel<NH>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                Shape<NH>::SMEM) == hipSuccess
+                ? 1
+                : -1;
+  return state > 0;
+}
+
+template <int NH>
+void launch_nh(const GemmArgs &g, const AttnArgs &a, const int32_t *order, hipStream_t s) {
+  const int grid = NXCD * 3 * (a.nh / NH) * ((a.B + NXCD - 1) / NXCD);
+  qkv_attn_kernel<NH><<<grid, 512 * NH, Shape<NH>::SMEM, s>>>(g, a, order);
+}
+
+}  // namespace
+
+// One head a workgroup; two (1,024 threads) with IXH_QKV_HEADS=2 when the
+// head count is even and the device grants the LDS. Two heads halve the
+// rows brought into LDS per head, but one workgroup then fills a CU and its
+// dequantisation and Attn8.Prepare phases (40% of a workgroup's time) no
+// longer overlap another workgroup's K loop: slower on cfg4 (339 against
+// 315 us a launch).
 void launch_qkv_attn(const GemmArgs &g, const AttnArgs &a, const int32_t *order, hipStream_t s) {
   if (a.B <= 0) return;
-  const int grid = NXCD * 3 * a.nh * ((a.B + NXCD - 1) / NXCD);
-  static bool attr_set = false;
-  if (!attr_set) {
-    (void)hipFuncSetAttribute((const void *)qkv_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
-    attr_set = true;
+  const char *e = getenv("IXH_QKV_HEADS");
+  const bool pair = e && e[0] == '2' && a.nh % 2 == 0;
+  if (pair && smem_ready<2>()) {
+    launch_nh<2>(g, a, order, s);
+  } else {
+    (void)smem_ready<1>();
+    launch_nh<1>(g, a, order, s);
   }
-  qkv_attn_kernel<<<grid, 512, SMEM, s>>>(g, a, order);
 }
 
 }  // namespace ixh

@@ -223,3 +223,21 @@ def test_split_streams_exact(parts, monkeypatch):
     assert f32_bits_equal(got, want), mismatch_report(got, want)
     pooled = gpu.encode_seqs(seqs)
     assert f32_bits_equal(pooled, ora.encode_seqs(seqs))
+
+
+@pytest.mark.parametrize("heads_env", ["2", "1"])
+def test_qkv_heads_per_workgroup(heads_env, monkeypatch):
+    """The fused QKV kernel with two heads a workgroup (IXH_QKV_HEADS=2:
+    1,024 threads, a 3-stage ring) and with one (the default), at lengths
+    around its 32-row blocks and the 256-row slab, up to 512."""
+    monkeypatch.setenv("IXH_QKV_HEADS", heads_env)
+    cfg = base_cfg(layers=2)
+    w, gpu, ora = model_pair(cfg, seed=31)
+    rng = np.random.default_rng(31)
+    seqs = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32)
+            for n in (1, 31, 32, 33, 255, 256, 257, 300, 511, 512, 0, 64)]
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+    pooled = gpu.encode_seqs(seqs)
+    assert f32_bits_equal(pooled, ora.encode_seqs(seqs))
