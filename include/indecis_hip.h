@@ -159,6 +159,18 @@ int ixh_tokenizer_encode_batch(const ixh_tokenizer *t,
                                int n, int max_len, int threads, int32_t *ids,
                                int64_t cap, int32_t *offs);
 
+/* Model.Embed (open.go:118-155): each text through EncodeMax(text,
+ * max_len), the encoder's pooled row, scaled to norm 1 by
+ * float32(1 / sqrt(max(sum of float64 squares, 1e-24))): out [n][H]. The
+ * tokenizer runs on `threads` host threads (0: one per core). The
+ * reference's embedding cache (WithEmbedCache) stays with the caller. */
+int ixh_embed_texts(ixh_model *m, const ixh_tokenizer *t,
+                    const char *const *texts, const int64_t *lens, int n,
+                    int max_len, int threads, float *out);
+/* The normalisation of Model.embed (open.go:134-146) on n rows of H
+ * floats, in place (host only). */
+int ixh_embed_normalize(float *rows, int n, int H);
+
 /* Optional: RoPE tables as Go's ropeFor computes them (model.go:256-277),
  * cos/sin [rows][head_dim/2], for the global (is_global=1) or local theta.
  * Without them the library computes the same formula with the C library's

@@ -21,6 +21,7 @@ EXPORTS = [
     "ixh_matmul8_outliers", "ixh_linear8", "ixh_model_load_safetensors", "ixh_safetensors_tensor",
     "ixh_tokenizer_load", "ixh_tokenizer_destroy", "ixh_tokenizer_info", "ixh_tokenizer_encode",
     "ixh_tokenizer_encode_pair", "ixh_tokenizer_encode_offsets", "ixh_tokenizer_encode_batch",
+    "ixh_embed_texts", "ixh_embed_normalize",
     "ixh_matmul8_tile", "ixh_layernorm_quant", "ixh_ln_matmul8_geglu", "ixh_attend8",
     "ixh_model_set_profiling", "ixh_model_set_profile_filter", "ixh_model_profile",
     "ixh_check_exp255", "ixh_batcher_create", "ixh_batcher_encode", "ixh_batcher_stats",
@@ -97,6 +98,8 @@ def lib():
                                       C.POINTER(C.c_int64)],
         "ixh_tokenizer_encode_offsets": [vp, C.c_char_p, C.c_int64, vp, vp, vp, C.c_int64, C.POINTER(C.c_int64)],
         "ixh_tokenizer_encode_batch": [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int64, vp],
+        "ixh_embed_texts": [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp],
+        "ixh_embed_normalize": [vp, C.c_int, C.c_int],
         "ixh_safetensors_tensor": [C.c_char_p, C.c_char_p, vp, C.c_int64, C.POINTER(C.c_int64)],
         "ixh_linear8": [vp, vp, vp, C.c_int, vp, C.c_int, C.c_float],
         "ixh_matmul8_tile": [vp, vp, C.c_int, vp, vp, vp],

@@ -4,8 +4,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 struct ixh_model;   // include/indecis_hip.h
 struct ixh_config;
+struct ixh_tokenizer;
 
 namespace ixh {
 
@@ -67,6 +70,9 @@ bool launch_gemm_ws(int epi, const GemmArgs &a, hipStream_t s);
 // ---- host helpers (ixh_api.cpp) ---------------------------------------------
 // Sets the calling thread's ixh_last_error message; returns code.
 int set_error(int code, const char *msg);
+// EncodeMax of n texts on worker threads, one id vector a text (tokenizer.cpp).
+int tokenize_texts(const ixh_tokenizer *t, const char *const *texts, const int64_t *lens, int n, int max_len,
+                   int threads, std::vector<std::vector<int32_t>> &per);
 // The config a model handle was created with.
 void model_config(const ::ixh_model *m, ::ixh_config *out);
 

@@ -850,15 +850,20 @@ int ixh_tokenizer_encode_offsets(const ixh_tokenizer *t, const char *text, int64
   return IXH_OK;
 }
 
-int ixh_tokenizer_encode_batch(const ixh_tokenizer *t, const char *const *texts, const int64_t *lens, int n,
-                               int max_len, int threads, int32_t *ids, int64_t cap, int32_t *offs) {
-  if (!t || n < 0 || (n > 0 && (!texts || !lens || !offs))) return set_error(IXH_EINVAL, "tokenizer: bad arguments");
+}  // extern "C"
+
+namespace ixh {
+
+// EncodeMax of n texts on `threads` worker threads (0: one per core), one
+// id vector a text; the arguments checked as the batch entry documents.
+int tokenize_texts(const ixh_tokenizer *t, const char *const *texts, const int64_t *lens, int n, int max_len,
+                   int threads, std::vector<std::vector<int32_t>> &per) {
+  if (!t || n < 0 || (n > 0 && (!texts || !lens))) return set_error(IXH_EINVAL, "tokenizer: bad arguments");
   for (int i = 0; i < n; i++)
     if (lens[i] < 0 || (!texts[i] && lens[i] > 0)) return set_error(IXH_EINVAL, "tokenizer: bad text");
-  offs[0] = 0;
+  per.assign(n, {});
   if (n == 0) return IXH_OK;
   const int nt = std::max(1, std::min(threads > 0 ? threads : (int)std::thread::hardware_concurrency(), n));
-  std::vector<std::vector<int32_t>> per(n);
   auto work = [&](int w) {
     Scratch sc;
     std::vector<int32_t> a;
@@ -868,6 +873,21 @@ int ixh_tokenizer_encode_batch(const ixh_tokenizer *t, const char *const *texts,
   for (int w = 1; w < nt; w++) pool.emplace_back(work, w);
   work(0);
   for (auto &th : pool) th.join();
+  return IXH_OK;
+}
+
+}  // namespace ixh
+
+extern "C" {
+
+int ixh_tokenizer_encode_batch(const ixh_tokenizer *t, const char *const *texts, const int64_t *lens, int n,
+                               int max_len, int threads, int32_t *ids, int64_t cap, int32_t *offs) {
+  if (n > 0 && !offs) return set_error(IXH_EINVAL, "tokenizer: bad arguments");
+  std::vector<std::vector<int32_t>> per;
+  int rc = ixh::tokenize_texts(t, texts, lens, n, max_len, threads, per);
+  if (rc) return rc;
+  if (offs) offs[0] = 0;
+  if (n == 0) return IXH_OK;
   int64_t total = 0;
   for (int i = 0; i < n; i++) {
     total += (int64_t)per[i].size();

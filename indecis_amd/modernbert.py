@@ -265,6 +265,19 @@ class Model:
         _lib.check(self._L.ixh_encode_seqs(self._h, _ptr(ids), _ptr(offs), len(seqs), _ptr(out)))
         return out[:len(seqs)]
 
+    def embed(self, tokenizer, texts, max_len=256, threads=0):
+        """Model.Embed (open.go:118-155): [n, H] embeddings of norm 1, each
+        text through EncodeMax(text, max_len) (max_len 256 as Open sets
+        it, model.go:265) on `threads` host threads, then the encoder."""
+        bs = [t.encode("utf-8") if isinstance(t, str) else bytes(t) for t in texts]
+        n = len(bs)
+        arr = (C.c_char_p * max(n, 1))(*bs)
+        lens = np.array([len(b) for b in bs] or [0], np.int64)
+        out = np.zeros((max(n, 1), self.cfg.hidden), np.float32)
+        _lib.check(self._L.ixh_embed_texts(self._h, tokenizer._h, C.cast(arr, C.c_void_p), _ptr(lens), n,
+                                           max_len, threads, _ptr(out)))
+        return out[:n]
+
     def encode_tokens(self, seqs):
         """EncodeTokens (infer.go:293-299): [sum of lengths, H]."""
         ids, offs = _offsets(seqs)

@@ -366,3 +366,17 @@ def head_logits(x, w, b):
     z = np.zeros((T, rows), np.float64)
     lib().ixo_head_logits(x, T, H, _c(w, np.float32), _c(b, np.float32), rows, z)
     return z
+
+
+def embed_normalize(rows):
+    """Model.embed's scaling (open.go:134-146): per row, n = the float64
+    sum of float64 squares in column order, inv = float32(1 / sqrt(max(n,
+    1e-24))), each value times inv in float32. np.cumsum adds in order."""
+    x = np.asarray(rows, np.float32)
+    out = np.empty_like(x)
+    for i, r in enumerate(x):
+        d = r.astype(np.float64)
+        n = float(np.cumsum(d * d)[-1]) if r.size else 0.0
+        inv = np.float32(1.0 / np.sqrt(max(n, 1e-24)))
+        out[i] = r * inv
+    return out
