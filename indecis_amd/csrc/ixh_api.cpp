@@ -445,8 +445,9 @@ struct Prof {
   }
 };
 
-// Streams a large batch is split over: IXH_SPLIT=1 (one pass) .. 4; default 2
-// (read at every call: tuning and tests change it between calls).
+// Streams a large batch is split over: IXH_SPLIT=1 (one pass) .. 4 (read
+// at every call: tuning and tests change it between calls); by default see
+// split_parts.
 // GEMM dispatch: the A-stationary kernel (gemm_as.hip) for Wi + GeGLU and
 // the plain stores (IXH_GEMM_AS=0 turns it off), gemm_i8 for the residual
 // GEMMs Wo and WoMLP. IXH_GEMM_WS=1 runs those on the warp-specialised
@@ -466,10 +467,18 @@ void run_gemm(int epi, const GemmArgs &g, hipStream_t st) {
   launch_gemm(epi, g, st);
 }
 
-int split_parts() {
+// Parts of a batch of B sequences and N tokens on a model of hidden H (from
+// kSplitTokens tokens on): IXH_SPLIT when set; else three for a wide model
+// with many sequences to balance (at least 48K tokens, 24 sequences and H
+// 768: cfg4 2% faster than two), else two (three were 1-2% slower on eight
+// 8,192-token sequences, 8% on cfg3's H 256).
+int split_parts(int N, int B, int H) {
   const char *e = getenv("IXH_SPLIT");
-  const int v = e ? atoi(e) : 2;
-  return v < 1 ? 1 : v > 4 ? 4 : v;
+  if (e) {
+    const int v = atoi(e);
+    return v < 1 ? 1 : v > 4 ? 4 : v;
+  }
+  return N >= 48 * 1024 && B >= 24 && H >= 768 ? 3 : 2;
 }
 
 // What a forward pass issued but has not waited for: its profiling records
@@ -796,8 +805,8 @@ int forward_split(ixh_model *m, Workspace *w, Workspace *const *extra, int nextr
 struct ExtraWs {
   ixh_model *m;
   std::vector<Workspace *> ws;
-  ExtraWs(ixh_model *model, int N) : m(model) {
-    const int want = N >= kSplitTokens ? split_parts() - 1 : 0;
+  ExtraWs(ixh_model *model, int N, int B) : m(model) {
+    const int want = N >= kSplitTokens ? split_parts(N, B, model->cfg.hidden) - 1 : 0;
     for (int k = 0; k < want; k++) {
       Workspace *w = acquire(m);
       if (!w) break;  // fewer parts
@@ -835,7 +844,7 @@ int encode_host(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, in
   WsGuard wg{m, acquire(m)};
   Workspace *w = wg.w;
   if (!w) return fail(IXH_EHIP, "modernbert: hip: stream creation failed");
-  ExtraWs ex(m, N);
+  ExtraWs ex(m, N, B);
   hipStream_t st = w->stream;
   const size_t out_elems = kind == IXH_OUT_TOKENS ? (size_t)N * H : (size_t)B * H;
   if ((rc = w->ids.ensure(4 * (size_t)N)) || (rc = w->pooled.ensure(4 * out_elems))) return rc;
@@ -1089,7 +1098,7 @@ int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs, i
   check_ids_kernel<<<(N + 255) / 256, 256, 0, st>>>(d_ids, N, m->cfg.vocab, w->flag.as<int>());
   LAUNCHCK("check_ids");
   HIPCK(hipMemcpyAsync(w->flag_host.p, w->flag.p, 4, hipMemcpyDeviceToHost, st));
-  ExtraWs ex(m, N);
+  ExtraWs ex(m, N, B);
   rc = forward_split(m, w, ex.ws.data(), (int)ex.ws.size(), st, d_ids, offs, B, out_kind, d_out);
   HIPCK(hipStreamSynchronize(st));  // the verdict has landed (forward_split waited for it too)
   const int bad = *(const int *)w->flag_host.p;
