@@ -203,9 +203,11 @@ def tokenize(np, args):
         seqs = [bi[bo[k]:bo[k + 1]] for k in range(len(batch))]
         t_all, _ = rate(text_to_rows, args.steps)
         t_enc, _ = rate(lambda: model.encode_seqs(seqs), args.steps)
+        t_emb, _ = rate(lambda: model.embed(tok, batch, max_len=512, threads=threads), args.steps)
         model.close()
         e2e = {"texts": len(batch), "tokens": int(bo[-1]), "ms_text_to_rows": round(t_all * 1e3, 3),
-               "ms_ids_to_rows": round(t_enc * 1e3, 3),
+               "ms_ids_to_rows": round(t_enc * 1e3, 3), "ms_embed": round(t_emb * 1e3, 3),
+               "embed_texts_per_s": round(len(batch) / t_emb, 1),
                "note": "EncodeMax(512) of 256 documents on the host, then EncodeSeqs (host ids in, pooled rows "
                        "out) on the GPU, ModernBERT-base shape"}
     print(json.dumps({
