@@ -233,7 +233,7 @@ def main():
     ap.add_argument("--lanes", type=int, default=8)
     ap.add_argument("--cpu-tokens", type=int, default=24576,
                     help="tokens of the batch timed on the CPU baseline (0: skip)")
-    ap.add_argument("--parts", default="",
+    ap.add_argument("--parts", type=int, default=0,
                     help="run every phase with the batch in this many parts (profiling runs: 1)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one device copy of 512 MiB (PMC calibration)")
@@ -282,7 +282,7 @@ def main():
         model.encode_device(ids_d.data_ptr(), offs, out_d.data_ptr(), _lib.OUT_POOLED, stream)
 
     if args.parts:
-        os.environ["IXH_SPLIT"] = args.parts  # warm-up passes shaped as the measured ones
+        model.set_option("parts", args.parts)  # warm-up passes shaped as the measured ones
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -296,7 +296,7 @@ def main():
     # One untimed pass, the batch as one part (no concurrent kernels), with
     # every launch bracketed by events: the per-class breakdown and the
     # dominant class.
-    os.environ["IXH_SPLIT"] = args.parts or "1"
+    model.set_option("parts", args.parts or 1)
     model.set_profiling(True)
     step()
     torch.cuda.synchronize()
@@ -304,14 +304,10 @@ def main():
     dom = max(breakdown, key=lambda k: breakdown[k]["ms"])
 
     def timed(parts):
-        """K timed steps with the batch in `parts` parts ("" = the library's
+        """K timed steps with the batch in `parts` parts (0 = the library's
         default split); events around the dominant class's launches only
         (two per launch, on the stream each runs on)."""
-        parts = args.parts or parts
-        if parts:
-            os.environ["IXH_SPLIT"] = parts
-        else:
-            os.environ.pop("IXH_SPLIT", None)
+        model.set_option("parts", args.parts or parts)
         step()  # untimed: workspaces of this split
         model.set_profiling(True, only=dom)
         e0 = torch.cuda.Event(enable_timing=True)
@@ -330,9 +326,9 @@ def main():
 
     # Headline: the library's default (a large batch runs as parts on
     # several streams). Roofline: the dominant class running alone.
-    ms_per_step, gpu_ms, d_conc = timed("")
-    ms_alone, _, d = timed("1")
-    os.environ.pop("IXH_SPLIT", None)
+    ms_per_step, gpu_ms, d_conc = timed(0)
+    ms_alone, _, d = timed(1)
+    model.set_option("parts", 0)
 
     # per-class figures of the untimed pass (one step)
     kernels = {}

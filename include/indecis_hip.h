@@ -173,17 +173,41 @@ int ixh_embed_normalize(float *rows, int n, int H);
 
 /* Optional: RoPE tables as Go's ropeFor computes them (model.go:256-277),
  * cos/sin [rows][head_dim/2], for the global (is_global=1) or local theta.
- * Without them the library computes the same formula with the C library's
- * pow/cos/sin. */
+ * They are used as given and never replaced: a batch whose longest
+ * sequence exceeds `rows` fails (IXH_EINVAL) until the caller uploads
+ * ropeFor(theta, n) for it. Without them (or after a call with NULL, NULL,
+ * 0) the library computes the same formula with the C library's
+ * pow/cos/sin, growing the tables to max(n, 512) rows as ropeFor does. */
 int ixh_model_set_rope(ixh_model *m, int is_global, const float *cos_t,
                        const float *sin_t, int rows);
+
+/* Kernel and pass choices of a model handle (no counterpart in the
+ * reference, whose only knob is the worker count, linalg.SetWorkers).
+ * Results never depend on them (the tests check every choice against the
+ * oracle); they only move time. Each call reads the handle's values once. */
+enum {
+  IXH_OPT_PARTS = 0,       /* streams a large batch is split over: 0 auto (default), 1..4 */
+  IXH_OPT_PASS_TOKENS = 1, /* most tokens of one pass, 1..131072 (default): larger
+                              batches run as several passes of whole sequences */
+  IXH_OPT_QKV_FUSED = 2,   /* 1 (default): QKV GEMM fused with Attn8.Prepare for
+                              sequences <= 512 keys; 0: two kernels */
+  IXH_OPT_QKV_HEADS = 3,   /* heads a workgroup of the fused QKV kernel: 1 (default) or 2 */
+  IXH_OPT_GEMM = 4,        /* 0 (default): A-stationary GEMM for Wi and plain stores;
+                              1: the tiled GEMM only; 2: as 0, residual GEMMs warp-specialised */
+  IXH_OPT_GEMM_TILE = 5,   /* tiled GEMM: 0 (default) 128x128 2 stages, 1 256x128 3, 2 128x128 3 */
+  IXH_OPT_LN_SEG = 6,      /* LayerNorm at lanes 8/16: 1 (default) segment kernel, 0 whole-row */
+};
+int ixh_model_set_option(ixh_model *m, int option, int64_t value);
+int ixh_model_get_option(ixh_model *m, int option, int64_t *value);
 
 /* Drops the uploaded weights (Invalidate/SetInt8, infer.go:95-135): the
  * next encode fails with IXH_ESTATE until they are set again. */
 int ixh_model_invalidate(ixh_model *m);
 
 /* EncodeSeqs (infer.go:261-289): ids of B sequences laid end to end,
- * offs[B+1] cumulative (offs[0] = 0), out [B][H] pooled (mean or CLS). */
+ * offs[B+1] cumulative (offs[0] = 0), out [B][H] pooled (mean or CLS).
+ * A batch over the pass size (IXH_OPT_PASS_TOKENS) runs as several passes
+ * of whole sequences; a single sequence over 131072 tokens is refused. */
 int ixh_encode_seqs(ixh_model *m, const int32_t *ids, const int32_t *offs,
                     int B, float *out);
 /* EncodeTokens (infer.go:293-299): out [offs[B]][H] final states. */
@@ -239,6 +263,28 @@ int ixh_model_set_profile_filter(ixh_model *m, const char *kernel_class);
  * classes. */
 int ixh_model_profile(ixh_model *m, ixh_kernel_stat *out, int cap, int *n);
 
+/* The model's decision heads, resident on its GPU (newHead/head.logits,
+ * heads.go:29-74): head h has rows[h] weight rows w[h] [rows[h]][H] and
+ * biases b[h] [rows[h]]; per_token[h] != 0 marks a Spans head, whose
+ * logits are taken of every token's state (spans.go:449-459), 0 a head of
+ * the pooled row. n = 0 removes them. Thread-safe; a pass in flight keeps
+ * the heads it started with. */
+int ixh_model_set_heads(ixh_model *m, int n, const int *rows,
+                        const int *per_token, const float *const *w,
+                        const float *const *b);
+/* infer's GPU half (spans.go:369-470, model.go:316-330) for a group of
+ * sequences (EncodeSeqs's ids/offs): the encoder pass, then on the device
+ *   pooled_z [B][Rp]: for each sequence the logits of the pooled-row heads
+ *     in order (Rp = the sum of their rows), z = sum_i f64(w) f64(x) + b,
+ *     on the pooled row of EncodeSeqs (the config's pooling) or, with
+ *     mean != 0, on the mean of its states (meanRows, spans.go:466-476, as
+ *     infer pools for a model with Spans questions);
+ *   token_z [N][Rt]: each token's logits of the per-token heads.
+ * Either output may be NULL (not computed). Batches over the pass size run
+ * as several passes; only the logits leave the GPU. */
+int ixh_encode_heads(ixh_model *m, const int32_t *ids, const int32_t *offs,
+                     int B, int mean, double *pooled_z, double *token_z);
+
 /* head.logits (heads.go:63-74) on host rows: z[t][r] = sum_i
  * f64(w[r][i]) f64(x[t][i]) + f64(b[r]), computed on the model's GPU. */
 int ixh_head_logits(ixh_model *m, const float *x, int T, const float *w,
@@ -251,6 +297,8 @@ int ixh_head_logits(ixh_model *m, const float *x, int T, const float *w,
 int ixh_packb8_create(int device, const int8_t *q, const float *scale, int k,
                       int n, int layout, ixh_packed_b8 **out);
 void ixh_packb8_destroy(ixh_packed_b8 *b);
+/* IXH_OPT_GEMM / IXH_OPT_GEMM_TILE for the linalg calls on this handle. */
+int ixh_packb8_set_option(ixh_packed_b8 *b, int option, int64_t value);
 
 /* MatMul8N (linalg/int8.go:89-155): c[m][n] (+)= a[m][k] . B, a quantised
  * per row as quantizeA does. Host buffers. */

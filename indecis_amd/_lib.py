@@ -25,7 +25,8 @@ EXPORTS = [
     "ixh_matmul8_tile", "ixh_layernorm_quant", "ixh_ln_matmul8_geglu", "ixh_attend8",
     "ixh_model_set_profiling", "ixh_model_set_profile_filter", "ixh_model_profile",
     "ixh_check_exp255", "ixh_batcher_create", "ixh_batcher_encode", "ixh_batcher_stats",
-    "ixh_batcher_destroy",
+    "ixh_batcher_destroy", "ixh_model_set_option", "ixh_model_get_option", "ixh_packb8_set_option",
+    "ixh_model_set_heads", "ixh_encode_heads",
 ]
 
 IXH_OK, IXH_EINVAL, IXH_ERANGE, IXH_ESTATE, IXH_EHIP, IXH_ENOMEM, IXH_EFORMAT = range(7)
@@ -34,6 +35,11 @@ MAT_QKV, MAT_O, MAT_I, MAT_OMLP = range(4)
 NORM_EMB, NORM_ATTN, NORM_MLP, NORM_FINAL = range(4)
 LAYOUT_ROWS, LAYOUT_PANELS = 0, 1
 OUT_POOLED, OUT_TOKENS = 0, 1
+(OPT_PARTS, OPT_PASS_TOKENS, OPT_QKV_FUSED, OPT_QKV_HEADS, OPT_GEMM, OPT_GEMM_TILE,
+ OPT_LN_SEG) = range(7)
+OPTIONS = {"parts": OPT_PARTS, "pass_tokens": OPT_PASS_TOKENS, "qkv_fused": OPT_QKV_FUSED,
+           "qkv_heads": OPT_QKV_HEADS, "gemm": OPT_GEMM, "gemm_tile": OPT_GEMM_TILE,
+           "ln_seg": OPT_LN_SEG}
 
 
 class IxhError(RuntimeError):
@@ -114,6 +120,11 @@ def lib():
         "ixh_batcher_create": [vp, C.c_int, C.c_int, C.POINTER(vp)],
         "ixh_batcher_encode": [vp, vp, vp, C.c_int, vp],
         "ixh_batcher_stats": [vp, C.POINTER(C.c_int64), C.POINTER(C.c_int64)],
+        "ixh_model_set_option": [vp, C.c_int, C.c_int64],
+        "ixh_model_get_option": [vp, C.c_int, C.POINTER(C.c_int64)],
+        "ixh_packb8_set_option": [vp, C.c_int, C.c_int64],
+        "ixh_model_set_heads": [vp, C.c_int, vp, vp, vp, vp],
+        "ixh_encode_heads": [vp, vp, vp, C.c_int, C.c_int, vp, vp],
     }
     for name, args in sig.items():
         f = getattr(L, name)

@@ -202,7 +202,9 @@ __global__ __launch_bounds__(256, 2) void gemm_as_kernel(GemmArgs a, int units, 
       zc[jj] = a.zc[col];
       sb[jj] = a.sb[col];
     }
-    crs = buf_rsrc(cbase + (size_t)p_m0 * ldc * 4, (uint32_t)(a.M - p_m0) * ldc * 4);
+    // the block's own rows only (at most BM * ldc * 4 bytes, far below 2^31):
+    // stores past row M fall outside and are dropped
+    crs = buf_rsrc(cbase + (size_t)p_m0 * ldc * 4, (uint32_t)min(a.M - p_m0, BM) * ldc * 4);
     if constexpr (EPI == EPI_GEGLU) {
       const int gc = n / 2 + fr;
       pvo[0] = gc < a.n_valid ? (uint32_t)(4 * fh * ldc + gc) * 4 : 0x80000000u;

@@ -353,13 +353,7 @@ void launch_cfg(int epi, const GemmArgs &a, hipStream_t s) {
 
 void launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
   if (a.M <= 0) return;
-  int cfg = a.tile_cfg;
-  if (cfg == 0) {
-    // IXH_GEMM_TILE=1|2 selects another tile configuration (tuning and tests)
-    const char *e = getenv("IXH_GEMM_TILE");
-    if (e) cfg = atoi(e);
-  }
-  switch (cfg) {
+  switch (a.tile_cfg) {
   case 1: launch_cfg<4, 3>(epi, a, s); break;
   case 2: launch_cfg<2, 3>(epi, a, s); break;
   default: launch_cfg<2, 2>(epi, a, s); break;

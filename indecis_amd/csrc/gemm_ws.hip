@@ -120,7 +120,9 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmArgs a, int units, int
     p_m0 = m0;
     p_n = n;
     p_par = tpar;
-    crs = buf_rsrc(cbase + (size_t)m0 * ldc * 4, (uint32_t)(a.M - m0) * ldc * 4);
+    // the block's own rows only (at most BM * ldc * 4 bytes): rows past M
+    // fall outside and are dropped
+    crs = buf_rsrc(cbase + (size_t)m0 * ldc * 4, (uint32_t)min(a.M - m0, BM) * ldc * 4);
     const int col = EPI == EPI_GEGLU ? n / 2 + 4 * cg : n + 4 * cg;
     pvo = col < a.n_valid ? (uint32_t)(rg * ldc + col) * 4 : 0x80000000u;
     if constexpr (ACC_IN) {

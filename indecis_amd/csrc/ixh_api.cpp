@@ -53,6 +53,11 @@ int fail(int code, const char *fmt, ...) {
 
 inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
+// Upper bound of Tuning::pass_tokens, and the longest sequence one pass
+// takes: every byte offset of a pass's buffers then fits in 31 bits
+// (N * 3H * 4 bytes at H 768 is 1.2 GB).
+constexpr int kMaxPassTokensOpt = 131072;
+
 // Device buffer that grows and never shrinks.
 struct DevBuf {
   void *p = nullptr;
@@ -214,11 +219,39 @@ struct RopeTab {
   std::shared_ptr<DevBuf> cos_t, sin_t;
 };
 
+// Decision heads resident on the device (ixh_model_set_heads): the
+// pooled-row heads' weight rows end to end, then the per-token heads'.
+struct HeadSet {
+  int rp = 0, rt = 0;     // rows of the pooled-row heads, of the per-token heads
+  DevBuf wp, bp, wt, bt;  // [rows][H] weights, [rows] biases
+};
+
+// What a pass writes (device pointers; null: not wanted). states [N][H]
+// final states (EncodeTokens); pooled [B][H] (EncodeSeqs); zp [B][rp]
+// pooled-row head logits; zt [N][rt] per-token head logits. mean: pool by
+// the mean whatever the config (meanRows, spans.go:466-476).
+struct Outputs {
+  float *states = nullptr;
+  float *pooled = nullptr;
+  double *zp = nullptr, *zt = nullptr;
+  int mean = 0;
+  // the outputs of sequences [b0, ...) whose first token is t0
+  Outputs at(int b0, int t0, int H, const HeadSet *hs) const {
+    Outputs o = *this;
+    if (o.states) o.states += (size_t)t0 * H;
+    if (o.pooled) o.pooled += (size_t)b0 * H;
+    if (o.zp) o.zp += (size_t)b0 * hs->rp;
+    if (o.zt) o.zt += (size_t)t0 * hs->rt;
+    return o;
+  }
+};
+
 struct Workspace {
   hipStream_t stream = nullptr;
   // tabs: the pass's small host-built tables, one copy: offs [B+1], padoff
   // [B+1], blocks [2 nblocks], sequence order [B]
   DevBuf ids, tabs, pos, x, xn, qkv, xq, sa, qq, sq, kp, ks, vt, vs, ctx, g, pooled, flag;
+  DevBuf out_states, out_pooled, out_zp, out_zt;  // host-path staging of a pass's outputs
   PinBuf host, flag_host;
   std::vector<hipEvent_t> events;  // profiling: begin/end pairs, reused
   hipEvent_t order[2] = {nullptr, nullptr};  // cross-stream ordering (no timing)
@@ -254,10 +287,14 @@ struct ixh_model {
   DevBuf emb_table, emb_exact_slot, emb_exact_rows, emb_i8_scale;
   std::mutex rope_mu;
   RopeTab rope[2];  // 0 local, 1 global
+  std::mutex heads_mu;
+  std::shared_ptr<HeadSet> heads;  // null: none set
   std::vector<std::shared_ptr<DevBuf>> rope_graveyard;
   std::mutex pool_mu;
   std::vector<Workspace *> pool;
   std::atomic<bool> weights_valid{true};
+  std::mutex tune_mu;
+  Tuning tuning;
   std::atomic<bool> profiling{false};
   std::mutex prof_mu;
   std::string prof_only;  // profile only this kernel class (empty: all)
@@ -275,9 +312,65 @@ struct ixh_packed_b8 {
   std::mutex mu;
   Mat geglu;
   bool geglu_set = false;
+  Tuning tuning;  // gemm, gemm_tile (guarded by mu)
 };
 
 namespace {
+
+// One option of ixh_model_set_option / ixh_packb8_set_option; model_opts:
+// the encoder options are allowed (a PackedB8 handle takes only the GEMM
+// choices).
+int set_tuning(Tuning &t, int option, int64_t v, bool model_opts) {
+  auto bad = [&]() { return fail(IXH_EINVAL, "indecis: option %d: value %lld out of range", option, (long long)v); };
+  switch (option) {
+  case IXH_OPT_GEMM:
+    if (v < 0 || v > 2) return bad();
+    t.gemm = (int)v;
+    return IXH_OK;
+  case IXH_OPT_GEMM_TILE:
+    if (v < 0 || v > 2) return bad();
+    t.gemm_tile = (int)v;
+    return IXH_OK;
+  default: break;
+  }
+  if (!model_opts) return fail(IXH_EINVAL, "linalg: option %d does not apply to a PackedB8", option);
+  switch (option) {
+  case IXH_OPT_PARTS:
+    if (v < 0 || v > 4) return bad();
+    t.parts = (int)v;
+    return IXH_OK;
+  case IXH_OPT_PASS_TOKENS:
+    if (v < 1 || v > kMaxPassTokensOpt) return bad();
+    t.pass_tokens = (int)v;
+    return IXH_OK;
+  case IXH_OPT_QKV_FUSED:
+    if (v != 0 && v != 1) return bad();
+    t.qkv_fused = (int)v;
+    return IXH_OK;
+  case IXH_OPT_QKV_HEADS:
+    if (v != 1 && v != 2) return bad();
+    t.qkv_heads = (int)v;
+    return IXH_OK;
+  case IXH_OPT_LN_SEG:
+    if (v != 0 && v != 1) return bad();
+    t.ln_seg = (int)v;
+    return IXH_OK;
+  default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
+  }
+}
+
+int get_tuning(const Tuning &t, int option, int64_t *v) {
+  switch (option) {
+  case IXH_OPT_PARTS: *v = t.parts; return IXH_OK;
+  case IXH_OPT_PASS_TOKENS: *v = t.pass_tokens; return IXH_OK;
+  case IXH_OPT_QKV_FUSED: *v = t.qkv_fused; return IXH_OK;
+  case IXH_OPT_QKV_HEADS: *v = t.qkv_heads; return IXH_OK;
+  case IXH_OPT_GEMM: *v = t.gemm; return IXH_OK;
+  case IXH_OPT_GEMM_TILE: *v = t.gemm_tile; return IXH_OK;
+  case IXH_OPT_LN_SEG: *v = t.ln_seg; return IXH_OK;
+  default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
+  }
+}
 
 int validate_config(const ixh_config &c) {
   if (c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.intermediate <= 0 || c.vocab <= 0)
@@ -315,12 +408,21 @@ int weights_ready(const ixh_model *m) {
   return IXH_OK;
 }
 
-// Tables covering at least `rows` positions (size max(rows, 512) as
-// ropeFor), returned as device pointers kept alive by `hold`.
+// Tables covering at least `rows` positions, returned as device pointers
+// kept alive by `hold`. The library's own tables (the ropeFor formula with
+// the C library's pow/cos/sin) grow to max(rows, 512) positions as ropeFor
+// does (model.go:256-277). A caller's tables (ixh_model_set_rope: Go's own
+// ropeFor output) are used as given and never replaced: a batch longer
+// than they are fails, and the caller uploads ropeFor(theta, n) first.
 int rope_for(ixh_model *m, int global, int rows, const float **c, const float **s,
              std::vector<std::shared_ptr<DevBuf>> &hold) {
   std::lock_guard<std::mutex> lk(m->rope_mu);
   RopeTab &t = m->rope[global];
+  if (t.user && t.rows < rows)
+    return fail(IXH_EINVAL,
+                "modernbert: hip: the %s RoPE table set by ixh_model_set_rope has %d rows, the batch "
+                "needs %d (upload ropeFor(theta, %d))",
+                global ? "global" : "local", t.rows, rows, rows);
   if (t.rows < rows || !t.cos_t) {
     const int size = std::max(rows, 512);
     std::vector<float> hc, hs;
@@ -371,6 +473,18 @@ struct WsGuard {
     if (w) release(m, w);
   }
 };
+
+__global__ void fill_u32_kernel(uint32_t *p, uint32_t v, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+// A fill kernel rather than hipMemsetAsync: the calls around it may be
+// captured into a HIP graph by the caller.
+void launch_fill_u32(void *p, uint32_t v, size_t n, hipStream_t st) {
+  if (n == 0) return;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
+  fill_u32_kernel<<<(unsigned)blocks, 256, 0, st>>>((uint32_t *)p, v, n);
+}
 
 __global__ void check_ids_kernel(const int32_t *ids, int N, int vocab, int *flag) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
@@ -445,39 +559,28 @@ struct Prof {
   }
 };
 
-// Streams a large batch is split over: IXH_SPLIT=1 (one pass) .. 4 (read
-// at every call: tuning and tests change it between calls); by default see
-// split_parts.
-// GEMM dispatch: the A-stationary kernel (gemm_as.hip) for Wi + GeGLU and
-// the plain stores (IXH_GEMM_AS=0 turns it off), gemm_i8 for the residual
-// GEMMs Wo and WoMLP. IXH_GEMM_WS=1 runs those on the warp-specialised
-// kernel (gemm_ws.hip) instead: 2-3 us faster per launch on cfg4, but the
-// kernels around it ran slower and the whole pass lost 0.5-1 ms, so it is
-// not the default.
-bool env_is(const char *name, char v) {
-  const char *e = getenv(name);
-  return e && e[0] == v;
-}
-
-void run_gemm(int epi, const GemmArgs &g, hipStream_t st) {
+// GEMM dispatch (Tuning::gemm): the A-stationary kernel (gemm_as.hip) for
+// Wi + GeGLU and the plain stores unless 1, gemm_i8 for the residual GEMMs
+// Wo and WoMLP. 2 runs those on the warp-specialised kernel (gemm_ws.hip)
+// instead: 2-3 us faster per launch on cfg4, but the kernels around it ran
+// slower and the whole pass lost 0.5-1 ms, so it is not the default.
+void run_gemm(int epi, const GemmArgs &g, const Tuning &t, hipStream_t st) {
   const bool as_epi = epi == EPI_GEGLU || epi == EPI_STORE || epi == EPI_TILE;
   const bool ws_epi = epi == EPI_ACCUM || epi == EPI_ACCUM_MLP;
-  if (as_epi && !env_is("IXH_GEMM_AS", '0') && launch_gemm_as(epi, g, st)) return;
-  if (ws_epi && env_is("IXH_GEMM_WS", '1') && launch_gemm_ws(epi, g, st)) return;
-  launch_gemm(epi, g, st);
+  if (as_epi && t.gemm != 1 && launch_gemm_as(epi, g, st)) return;
+  if (ws_epi && t.gemm == 2 && launch_gemm_ws(epi, g, st)) return;
+  GemmArgs gi = g;
+  gi.tile_cfg = t.gemm_tile;
+  launch_gemm(epi, gi, st);
 }
 
 // Parts of a batch of B sequences and N tokens on a model of hidden H (from
-// kSplitTokens tokens on): IXH_SPLIT when set; else three for a wide model
-// with many sequences to balance (at least 48K tokens, 24 sequences and H
-// 768: cfg4 2% faster than two), else two (three were 1-2% slower on eight
-// 8,192-token sequences, 8% on cfg3's H 256).
-int split_parts(int N, int B, int H) {
-  const char *e = getenv("IXH_SPLIT");
-  if (e) {
-    const int v = atoi(e);
-    return v < 1 ? 1 : v > 4 ? 4 : v;
-  }
+// kSplitTokens tokens on): Tuning::parts when set; else three for a wide
+// model with many sequences to balance (at least 48K tokens, 24 sequences
+// and H 768: cfg4 2% faster than two), else two (three were 1-2% slower on
+// eight 8,192-token sequences, 8% on cfg3's H 256).
+int split_parts(const Tuning &t, int N, int B, int H) {
+  if (t.parts > 0) return std::min(t.parts, 4);
   return N >= 48 * 1024 && B >= 24 && H >= 768 ? 3 : 2;
 }
 
@@ -491,8 +594,9 @@ struct Pending {
 // The forward pass. ids/out are device pointers here. With `defer` the
 // launches are only issued: the caller synchronises the stream, then calls
 // defer->prof->flush().
-int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
-            const int32_t *offs, int B, int out_kind, float *d_out, Pending *defer = nullptr) {
+int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w, hipStream_t st,
+            const int32_t *d_ids, const int32_t *offs, int B, const Outputs &out,
+            Pending *defer = nullptr) {
   const ixh_config &c = m->cfg;
   const int H = c.hidden, I = c.intermediate, nh = c.heads, D = m->D;
   const int N = offs[B];
@@ -517,9 +621,8 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   for (int b = 0; b < B; b++) order[b] = b;
   std::stable_sort(order.begin(), order.end(),
                    [&](int x, int y) { return offs[x + 1] - offs[x] > offs[y + 1] - offs[y]; });
-  // IXH_QKV_FUSED=0: QKV GEMM and attention prologue as two kernels (tests, timing)
-  const char *fe = getenv("IXH_QKV_FUSED");
-  const bool fused = T <= kQkvSeqMax && !(fe && fe[0] == '0');
+  // qkv_fused 0: QKV GEMM and attention prologue as two kernels (tests, timing)
+  const bool fused = T <= kQkvSeqMax && tune.qkv_fused != 0;
 
   int rc;
   const size_t ntab = 2 * (size_t)(B + 1) + blocks.size() + B;
@@ -579,6 +682,9 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   const double dN = N, dH = H, dI = I;
   const double row_bytes = m->emb_format == 0 ? 4 * dH : m->emb_format == 1 ? 2 * dH : dH + 4;
 
+  float *xn = out.states ? out.states : w->xn.as<float>();
+  // a part of empty sequences only: zero pooled rows (and their logits)
+  if (N > 0) {
   RUN("positions", 0, 8.0 * N,
       launch_positions(d_offs, d_padoff, B, w->pos.as<int32_t>(), nullptr, st));
 
@@ -603,6 +709,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   ra.q = w->xq.as<int8_t>();
   ra.ldq = KpH;
   ra.sa = w->sa.as<float>();
+  ra.seg = tune.ln_seg;
   RUN("emb_ln_quant", 0, dN * (4 + row_bytes + 4 * dH + dH + 4), launch_rownorm(ra, st));
 
   auto gemm = [&](int epi, const Mat &M, int Kp, float *C, int ldc, int n_valid) {
@@ -665,6 +772,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
   ln.q = w->xq.as<int8_t>();
   ln.ldq = KpH;
   ln.sa = w->sa.as<float>();
+  ln.seg = tune.ln_seg;
   const double ln_bytes = dN * (4 * dH + dH + 4);
 
   for (int l = 0; l < c.layers; l++) {
@@ -691,7 +799,7 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
       // scales are its only outputs
       RUN("gemm_qkv", 2 * dN * 3 * dH * dH,
           gemm_bytes(dH, 3 * dH, 0, false) + dN * (3 * dH + 8 * nh) + 4.0 * B * dH,
-          launch_qkv_attn(g, aa, d_order, st));
+          launch_qkv_attn(g, aa, d_order, tune.qkv_heads, st));
     } else {
       RUN("gemm_qkv", 2 * dN * 3 * dH * dH,
           gemm_bytes(dH, 3 * dH, 2 * dH, false) + dN * (4 + dH + 4 * nh), launch_gemm(EPI_ROPE, g, st));
@@ -705,20 +813,21 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     RUN("quant_ctx", 0, dN * (4 * dH + dH + 4),
         launch_quant_rows(w->ctx.as<float>(), H, N, H, w->xq.as<int8_t>(), KpH, w->sa.as<float>(), st));
     g = gemm(EPI_ACCUM, L.o, KpH, w->x.as<float>(), H, H);
-    RUN("gemm_wo", 2 * dN * dH * dH, gemm_bytes(dH, dH, dH, true), run_gemm(EPI_ACCUM, g, st));
+    RUN("gemm_wo", 2 * dN * dH * dH, gemm_bytes(dH, dH, dH, true), run_gemm(EPI_ACCUM, g, tune, st));
     // mlp_norm, Wi + GeGLU, x += g . WoMLP^T (infer.go:404-424)
     ln.gamma = L.mlp_norm.as<float>();
     RUN("ln_quant", 0, ln_bytes, launch_rownorm(ln, st));
     g = gemm(EPI_GEGLU, L.i, KpH, w->g.as<float>(), I, I);
     RUN("gemm_wi", 2 * dN * 2 * dI * dH, gemm_bytes(dH, 2 * dI, dI, false),
-        run_gemm(EPI_GEGLU, g, st));
+        run_gemm(EPI_GEGLU, g, tune, st));
     RUN("quant_g", 0, dN * (4 * dI + dI + 4),
         launch_quant_rows(w->g.as<float>(), I, N, I, w->xq.as<int8_t>(), KpI, w->sa.as<float>(), st));
     g = gemm(EPI_ACCUM_MLP, L.omlp, KpI, w->x.as<float>(), H, H);
     RUN("gemm_womlp", 2 * dN * dH * dI, gemm_bytes(dI, dH, dH, true),
-        run_gemm(EPI_ACCUM_MLP, g, st));
+        run_gemm(EPI_ACCUM_MLP, g, tune, st));
   }
-  // final_norm (infer.go:427), then pooling or the token states
+  // final_norm (infer.go:427), then the token states, pooling (infer.go:
+  // 265-287) and the heads' logits (heads.go:63-74) on the device
   {
     RowArgs r{};
     r.M = N;
@@ -727,12 +836,25 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
     r.gamma = m->final_norm.as<float>();
     r.eps = c.norm_eps;
     r.lanes = c.lanes;
-    r.out = out_kind == IXH_OUT_TOKENS ? d_out : w->xn.as<float>();
+    r.seg = tune.ln_seg;
+    r.out = xn;
     RUN("final_norm", 0, dN * 8 * dH, launch_rownorm(r, st));
   }
-  if (out_kind == IXH_OUT_POOLED)
+  }  // N > 0
+  float *pooled = out.pooled;
+  if (!pooled && out.zp) {
+    if ((rc = w->pooled.ensure(4 * (size_t)B * H))) return rc;
+    pooled = w->pooled.as<float>();
+  }
+  if (pooled)
     RUN("pool", 0, dN * 4 * dH + (double)B * 4 * dH,
-        launch_pool(w->xn.as<float>(), d_offs, B, H, c.pooling == IXH_POOL_CLS, d_out, st));
+        launch_pool(xn, d_offs, B, H, c.pooling == IXH_POOL_CLS && !out.mean, pooled, st));
+  if (out.zp && heads->rp > 0)
+    RUN("head_pooled", 0, (double)B * (4 * dH + 8 * heads->rp),
+        launch_head_logits(pooled, B, H, heads->wp.as<float>(), heads->bp.as<float>(), heads->rp, out.zp, st));
+  if (out.zt && heads->rt > 0 && N > 0)
+    RUN("head_tokens", 0, dN * (4 * dH + 8 * heads->rt),
+        launch_head_logits(xn, N, H, heads->wt.as<float>(), heads->bt.as<float>(), heads->rt, out.zt, st));
 #undef RUN
   if (defer) return prof.err;
   // tables used by queued work stay alive until the stream has run them
@@ -742,18 +864,21 @@ int forward(ixh_model *m, Workspace *w, hipStream_t st, const int32_t *d_ids,
 
 // Token count from which a batch is split over several streams.
 constexpr int kSplitTokens = 4096;
+constexpr int kMaxPassTokens = kMaxPassTokensOpt;
 
 // The batch as P parts of about equal token counts, each on its own stream
 // (the caller's, then those of extra workspaces), issued back to back: the
 // kernels of one part (say its GEMMs) share the CUs with those of another
 // (its attention or row kernels), which are bound by other resources.
 // Sequences are independent, so the results equal one pass's. Without
-// extra workspaces (or for a small batch): one pass.
-int forward_split(ixh_model *m, Workspace *w, Workspace *const *extra, int nextra, hipStream_t st,
-                  const int32_t *d_ids, const int32_t *offs, int B, int out_kind, float *d_out) {
+// extra workspaces (or for a small batch): one pass. Returns once st has
+// run every part.
+int forward_split(ixh_model *m, const Tuning &tune, const HeadSet *hs, Workspace *w,
+                  Workspace *const *extra, int nextra, hipStream_t st, const int32_t *d_ids,
+                  const int32_t *offs, int B, const Outputs &out) {
   const int N = offs[B];
   const int P = std::min(nextra + 1, B);
-  if (P < 2 || N < kSplitTokens) return forward(m, w, st, d_ids, offs, B, out_kind, d_out);
+  if (P < 2 || N < kSplitTokens) return forward(m, tune, hs, w, st, d_ids, offs, B, out);
   // part p covers sequences [cut[p], cut[p+1]): the first starting at or
   // past p*N/P
   std::vector<int> cut(P + 1, B);
@@ -784,9 +909,8 @@ int forward_split(ixh_model *m, Workspace *w, Workspace *const *extra, int nextr
     hipStream_t sp = p == 0 ? st : wp->stream;
     offp[p].resize(b1 - b0 + 1);
     for (int b = b0; b <= b1; b++) offp[p][b - b0] = offs[b] - offs[b0];
-    const size_t out_off = out_kind == IXH_OUT_POOLED ? (size_t)b0 * H : (size_t)offs[b0] * H;
-    const int r = forward(m, wp, sp, d_ids + offs[b0], offp[p].data(), b1 - b0, out_kind,
-                          d_out + out_off, &pend[p]);
+    const int r = forward(m, tune, hs, wp, sp, d_ids + offs[b0], offp[p].data(), b1 - b0,
+                          out.at(b0, offs[b0], H, hs), &pend[p]);
     if (r && !rc) rc = r;
   }
   // st waits for every part whatever happened, so nothing is left queued
@@ -801,12 +925,12 @@ int forward_split(ixh_model *m, Workspace *w, Workspace *const *extra, int nextr
   return IXH_OK;
 }
 
-// Extra workspaces for a split pass, returned to the pool on scope exit.
+// Extra workspaces for split passes, returned to the pool on scope exit.
 struct ExtraWs {
   ixh_model *m;
   std::vector<Workspace *> ws;
-  ExtraWs(ixh_model *model, int N, int B) : m(model) {
-    const int want = N >= kSplitTokens ? split_parts(N, B, model->cfg.hidden) - 1 : 0;
+  ExtraWs(ixh_model *model, const Tuning &t, int N, int B) : m(model) {
+    const int want = N >= kSplitTokens ? split_parts(t, N, B, model->cfg.hidden) - 1 : 0;
     for (int k = 0; k < want; k++) {
       Workspace *w = acquire(m);
       if (!w) break;  // fewer parts
@@ -827,33 +951,117 @@ int check_offs(const int32_t *offs, int B) {
   return IXH_OK;
 }
 
-int encode_host(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, int kind,
-                float *out) {
+// The handle's tuning, copied once per call.
+Tuning tuning_of(ixh_model *m) {
+  std::lock_guard<std::mutex> lk(m->tune_mu);
+  return m->tuning;
+}
+
+// Passes of whole sequences, in order, of at most t.pass_tokens tokens
+// each (a longer sequence takes a pass of its own): cut[i] .. cut[i+1].
+// Rows do not depend on their batch (TestMatMul8RowsIndependent), so the
+// results are those of one pass.
+int plan_passes(const Tuning &t, const int32_t *offs, int B, std::vector<int> &cut) {
+  cut.assign(1, 0);
+  for (int b = 0; b < B; b++) {
+    const int n = offs[b + 1] - offs[b];
+    if (n > kMaxPassTokens)
+      return fail(IXH_EINVAL, "modernbert: hip: sequence of %d tokens over the %d-token limit of a pass", n,
+                  kMaxPassTokens);
+    if (b > cut.back() && offs[b + 1] - offs[cut.back()] > t.pass_tokens) cut.push_back(b);
+  }
+  cut.push_back(B);
+  return IXH_OK;
+}
+
+// The heads the call needs (an error when out asks for logits and none
+// are set), kept alive by the returned pointer.
+int heads_for(ixh_model *m, bool want, std::shared_ptr<HeadSet> &hs) {
+  std::lock_guard<std::mutex> lk(m->heads_mu);
+  hs = m->heads;
+  if (want && !hs) return fail(IXH_ESTATE, "indecis: no heads set (ixh_model_set_heads)");
+  if (!hs) hs = std::make_shared<HeadSet>();
+  return IXH_OK;
+}
+
+// EncodeSeqs / EncodeTokens / the heads' logits from host ids into host
+// outputs (what `out` points at is host memory here), pass by pass.
+int encode_host(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, const Outputs &out) {
   if (!m) return fail(IXH_EINVAL, "modernbert: nil model");
   int rc;
   if ((rc = check_offs(offs, B))) return rc;
   const int N = B ? offs[B] : 0;
+  if (N > 0 && !ids) return fail(IXH_EINVAL, "modernbert: inconsistent batch");
   for (int t = 0; t < N; t++)
     if (ids[t] < 0 || ids[t] >= m->cfg.vocab)
       return fail(IXH_ERANGE, "modernbert: id %d out of vocabulary", ids[t]);
+  std::shared_ptr<HeadSet> hsp;
+  if ((rc = heads_for(m, out.zp || out.zt, hsp))) return rc;
+  const HeadSet *hs = hsp.get();
   const int H = m->cfg.hidden;
-  if (kind == IXH_OUT_POOLED && B > 0) memset(out, 0, sizeof(float) * (size_t)B * H);
+  DEVGUARD(m->device);
+  // empty sequences: zero pooled rows, whose logits are the biases (passes
+  // overwrite the rows of the others)
+  if (out.pooled && B > 0) memset(out.pooled, 0, sizeof(float) * (size_t)B * H);
+  if (out.zp && hs->rp > 0 && B > 0) {
+    std::vector<float> bp(hs->rp);
+    HIPCK(hipMemcpy(bp.data(), hs->bp.p, 4 * (size_t)hs->rp, hipMemcpyDeviceToHost));
+    for (int b = 0; b < B; b++)
+      for (int r = 0; r < hs->rp; r++) out.zp[(size_t)b * hs->rp + r] = (double)bp[r];
+  }
   if (N == 0) return IXH_OK;
   if ((rc = weights_ready(m))) return rc;
-  DEVGUARD(m->device);
+  const Tuning tune = tuning_of(m);
+  std::vector<int> cut;
+  if ((rc = plan_passes(tune, offs, B, cut))) return rc;
   WsGuard wg{m, acquire(m)};
   Workspace *w = wg.w;
   if (!w) return fail(IXH_EHIP, "modernbert: hip: stream creation failed");
-  ExtraWs ex(m, N, B);
+  int maxN = 0, maxB = 0;
+  for (size_t i = 0; i + 1 < cut.size(); i++) {
+    maxN = std::max(maxN, offs[cut[i + 1]] - offs[cut[i]]);
+    maxB = std::max(maxB, cut[i + 1] - cut[i]);
+  }
+  ExtraWs ex(m, tune, maxN, maxB);
   hipStream_t st = w->stream;
-  const size_t out_elems = kind == IXH_OUT_TOKENS ? (size_t)N * H : (size_t)B * H;
-  if ((rc = w->ids.ensure(4 * (size_t)N)) || (rc = w->pooled.ensure(4 * out_elems))) return rc;
-  HIPCK(hipMemcpyAsync(w->ids.p, ids, 4 * (size_t)N, hipMemcpyHostToDevice, st));
-  if ((rc = forward_split(m, w, ex.ws.data(), (int)ex.ws.size(), st, w->ids.as<int32_t>(), offs, B,
-                          kind, w->pooled.as<float>())))
-    return rc;
-  HIPCK(hipMemcpyAsync(out, w->pooled.p, 4 * out_elems, hipMemcpyDeviceToHost, st));
-  HIPCK(hipStreamSynchronize(st));
+  if ((rc = w->ids.ensure(4 * (size_t)maxN))) return rc;
+  Outputs dev;
+  dev.mean = out.mean;
+  if (out.states) {
+    if ((rc = w->out_states.ensure(4 * (size_t)maxN * H))) return rc;
+    dev.states = w->out_states.as<float>();
+  }
+  if (out.pooled) {
+    if ((rc = w->out_pooled.ensure(4 * (size_t)maxB * H))) return rc;
+    dev.pooled = w->out_pooled.as<float>();
+  }
+  if (out.zp && hs->rp > 0) {
+    if ((rc = w->out_zp.ensure(8 * (size_t)maxB * hs->rp))) return rc;
+    dev.zp = w->out_zp.as<double>();
+  }
+  if (out.zt && hs->rt > 0) {
+    if ((rc = w->out_zt.ensure(8 * (size_t)maxN * hs->rt))) return rc;
+    dev.zt = w->out_zt.as<double>();
+  }
+  std::vector<int32_t> offp;
+  for (size_t i = 0; i + 1 < cut.size(); i++) {
+    const int b0 = cut[i], b1 = cut[i + 1], t0 = offs[b0], n = offs[b1] - t0;
+    if (n == 0) continue;  // pooled rows and logits already set
+    offp.resize(b1 - b0 + 1);
+    for (int b = b0; b <= b1; b++) offp[b - b0] = offs[b] - t0;
+    HIPCK(hipMemcpyAsync(w->ids.p, ids + t0, 4 * (size_t)n, hipMemcpyHostToDevice, st));
+    if ((rc = forward_split(m, tune, hs, w, ex.ws.data(), (int)ex.ws.size(), st, w->ids.as<int32_t>(),
+                            offp.data(), b1 - b0, dev)))
+      return rc;
+    const Outputs h = out.at(b0, t0, H, hs);
+    if (dev.states) HIPCK(hipMemcpyAsync(h.states, dev.states, 4 * (size_t)n * H, hipMemcpyDeviceToHost, st));
+    if (dev.pooled)
+      HIPCK(hipMemcpyAsync(h.pooled, dev.pooled, 4 * (size_t)(b1 - b0) * H, hipMemcpyDeviceToHost, st));
+    if (dev.zp)
+      HIPCK(hipMemcpyAsync(h.zp, dev.zp, 8 * (size_t)(b1 - b0) * hs->rp, hipMemcpyDeviceToHost, st));
+    if (dev.zt) HIPCK(hipMemcpyAsync(h.zt, dev.zt, 8 * (size_t)n * hs->rt, hipMemcpyDeviceToHost, st));
+    HIPCK(hipStreamSynchronize(st));
+  }
   return IXH_OK;
 }
 
@@ -1004,7 +1212,14 @@ int ixh_model_set_embeddings_i8(ixh_model *m, const int8_t *table, const float *
 
 int ixh_model_set_rope(ixh_model *m, int is_global, const float *cos_t, const float *sin_t,
                        int rows) {
-  if (!m || !cos_t || !sin_t || rows <= 0) return fail(IXH_EINVAL, "modernbert: nil rope table");
+  if (!m) return fail(IXH_EINVAL, "modernbert: nil model");
+  if (!cos_t && !sin_t && rows == 0) {
+    // back to the library's own tables
+    std::lock_guard<std::mutex> lk(m->rope_mu);
+    m->rope[is_global ? 1 : 0] = RopeTab{};
+    return IXH_OK;
+  }
+  if (!cos_t || !sin_t || rows <= 0) return fail(IXH_EINVAL, "modernbert: nil rope table");
   DEVGUARD(m->device);
   const size_t bytes = 4 * (size_t)rows * (m->D / 2);
   auto nc = std::make_shared<DevBuf>(), ns = std::make_shared<DevBuf>();
@@ -1028,6 +1243,56 @@ int ixh_model_invalidate(ixh_model *m) {
     L.qkv.set = L.o.set = L.i.set = L.omlp.set = false;
   }
   return IXH_OK;
+}
+
+int ixh_model_set_heads(ixh_model *m, int n, const int *rows, const int *per_token,
+                        const float *const *w, const float *const *b) {
+  if (!m || n < 0 || (n > 0 && (!rows || !per_token || !w || !b)))
+    return fail(IXH_EINVAL, "indecis: heads: bad arguments");
+  const int H = m->cfg.hidden;
+  if (n == 0) {
+    std::lock_guard<std::mutex> lk(m->heads_mu);
+    m->heads.reset();
+    return IXH_OK;
+  }
+  std::vector<float> wp, bp, wt, bt;
+  for (int h = 0; h < n; h++) {
+    if (rows[h] <= 0 || !w[h] || !b[h]) return fail(IXH_EINVAL, "indecis: head %d: bad arguments", h);
+    std::vector<float> &W = per_token[h] ? wt : wp, &Bv = per_token[h] ? bt : bp;
+    W.insert(W.end(), w[h], w[h] + (size_t)rows[h] * H);
+    Bv.insert(Bv.end(), b[h], b[h] + rows[h]);
+  }
+  DEVGUARD(m->device);
+  auto hs = std::make_shared<HeadSet>();
+  hs->rp = (int)bp.size();
+  hs->rt = (int)bt.size();
+  int rc;
+  if ((rc = hs->wp.ensure(4 * wp.size())) || (rc = hs->bp.ensure(4 * bp.size())) ||
+      (rc = hs->wt.ensure(4 * wt.size())) || (rc = hs->bt.ensure(4 * bt.size())))
+    return rc;
+  if (!wp.empty()) {
+    HIPCK(hipMemcpy(hs->wp.p, wp.data(), 4 * wp.size(), hipMemcpyHostToDevice));
+    HIPCK(hipMemcpy(hs->bp.p, bp.data(), 4 * bp.size(), hipMemcpyHostToDevice));
+  }
+  if (!wt.empty()) {
+    HIPCK(hipMemcpy(hs->wt.p, wt.data(), 4 * wt.size(), hipMemcpyHostToDevice));
+    HIPCK(hipMemcpy(hs->bt.p, bt.data(), 4 * bt.size(), hipMemcpyHostToDevice));
+  }
+  std::lock_guard<std::mutex> lk(m->heads_mu);
+  m->heads = hs;
+  return IXH_OK;
+}
+
+int ixh_model_set_option(ixh_model *m, int option, int64_t value) {
+  if (!m) return fail(IXH_EINVAL, "modernbert: nil model");
+  std::lock_guard<std::mutex> lk(m->tune_mu);
+  return set_tuning(m->tuning, option, value, true);
+}
+
+int ixh_model_get_option(ixh_model *m, int option, int64_t *value) {
+  if (!m || !value) return fail(IXH_EINVAL, "modernbert: nil model");
+  std::lock_guard<std::mutex> lk(m->tune_mu);
+  return get_tuning(m->tuning, option, value);
 }
 
 int ixh_model_set_profiling(ixh_model *m, int on) {
@@ -1063,11 +1328,27 @@ int ixh_model_profile(ixh_model *m, ixh_kernel_stat *out, int cap, int *n) {
 }
 
 int ixh_encode_seqs(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, float *out) {
-  return encode_host(m, ids, offs, B, IXH_OUT_POOLED, out);
+  if (B > 0 && !out) return fail(IXH_EINVAL, "modernbert: nil output");
+  Outputs o;
+  o.pooled = out;
+  return encode_host(m, ids, offs, B, o);
 }
 
 int ixh_encode_tokens(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, float *out) {
-  return encode_host(m, ids, offs, B, IXH_OUT_TOKENS, out);
+  if (B > 0 && offs && offs[B] > 0 && !out) return fail(IXH_EINVAL, "modernbert: nil output");
+  Outputs o;
+  o.states = out;
+  return encode_host(m, ids, offs, B, o);
+}
+
+int ixh_encode_heads(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, int mean,
+                     double *pooled_z, double *token_z) {
+  if (!pooled_z && !token_z) return fail(IXH_EINVAL, "indecis: no output asked for");
+  Outputs o;
+  o.zp = pooled_z;
+  o.zt = token_z;
+  o.mean = mean != 0;
+  return encode_host(m, ids, offs, B, o);
 }
 
 int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs, int B,
@@ -1079,32 +1360,62 @@ int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs, i
   if ((rc = check_offs(offs, B))) return rc;
   const int N = B ? offs[B] : 0;
   const int H = m->cfg.hidden;
+  if (N > 0 && (rc = weights_ready(m))) return rc;
+  const Tuning tune = tuning_of(m);
+  std::vector<int> cut;
+  if ((rc = plan_passes(tune, offs, B, cut))) return rc;
   DEVGUARD(m->device);
   WsGuard wg{m, acquire(m)};
   Workspace *w = wg.w;
   if (!w) return fail(IXH_EHIP, "modernbert: hip: stream creation failed");
   hipStream_t st = stream ? (hipStream_t)stream : w->stream;
-  if (out_kind == IXH_OUT_POOLED && B > 0)
-    HIPCK(hipMemsetAsync(d_out, 0, 4 * (size_t)B * H, st));
-  if (N == 0) return IXH_OK;
-  if ((rc = weights_ready(m))) return rc;
+  const size_t out_elems = out_kind == IXH_OUT_TOKENS ? (size_t)N * H : (size_t)B * H;
+  if (N == 0) {
+    launch_fill_u32(d_out, 0u, out_elems, st);
+    LAUNCHCK("fill");
+    HIPCK(hipStreamSynchronize(st));
+    return IXH_OK;
+  }
   // ids on the device: checked by a kernel (infer.go:308-312) whose verdict
-  // is read once the pass has run — no wait before the pass. The gather
+  // is read once the passes have run — no wait before them. The gather
   // clamps ids into the table, so a bad batch computes garbage that is
   // then discarded: d_out is zeroed and the reference's error returned.
   if ((rc = w->flag.ensure(4)) || (rc = w->flag_host.ensure(4))) return rc;
-  const int big = 0x7f7f7f7f;  // the byte fill below: larger than any index
-  HIPCK(hipMemsetAsync(w->flag.p, 0x7f, 4, st));
+  const unsigned big = 0x7f7f7f7fu;  // larger than any index
+  launch_fill_u32(w->flag.p, big, 1, st);
   check_ids_kernel<<<(N + 255) / 256, 256, 0, st>>>(d_ids, N, m->cfg.vocab, w->flag.as<int>());
   LAUNCHCK("check_ids");
   HIPCK(hipMemcpyAsync(w->flag_host.p, w->flag.p, 4, hipMemcpyDeviceToHost, st));
-  ExtraWs ex(m, N, B);
-  rc = forward_split(m, w, ex.ws.data(), (int)ex.ws.size(), st, d_ids, offs, B, out_kind, d_out);
-  HIPCK(hipStreamSynchronize(st));  // the verdict has landed (forward_split waited for it too)
-  const int bad = *(const int *)w->flag_host.p;
+  int maxN = 0, maxB = 0;
+  for (size_t i = 0; i + 1 < cut.size(); i++) {
+    maxN = std::max(maxN, offs[cut[i + 1]] - offs[cut[i]]);
+    maxB = std::max(maxB, cut[i + 1] - cut[i]);
+  }
+  ExtraWs ex(m, tune, maxN, maxB);
+  HeadSet none;
+  Outputs out;
+  (out_kind == IXH_OUT_TOKENS ? out.states : out.pooled) = d_out;
+  std::vector<int32_t> offp;
+  for (size_t i = 0; i + 1 < cut.size() && !rc; i++) {
+    const int b0 = cut[i], b1 = cut[i + 1], t0 = offs[b0], n = offs[b1] - t0;
+    const Outputs o = out.at(b0, t0, H, &none);
+    if (n == 0) {
+      if (o.pooled) {
+        launch_fill_u32(o.pooled, 0u, (size_t)(b1 - b0) * H, st);
+        LAUNCHCK("fill");
+      }
+      continue;
+    }
+    offp.resize(b1 - b0 + 1);
+    for (int b = b0; b <= b1; b++) offp[b - b0] = offs[b] - t0;
+    rc = forward_split(m, tune, &none, w, ex.ws.data(), (int)ex.ws.size(), st, d_ids + t0, offp.data(),
+                       b1 - b0, o);
+  }
+  HIPCK(hipStreamSynchronize(st));  // the verdict has landed
+  const unsigned bad = *(const unsigned *)w->flag_host.p;
   if (bad != big) {
-    const size_t out_elems = out_kind == IXH_OUT_TOKENS ? (size_t)N * H : (size_t)B * H;
-    HIPCK(hipMemsetAsync(d_out, 0, 4 * out_elems, st));
+    launch_fill_u32(d_out, 0u, out_elems, st);
+    LAUNCHCK("fill");
     int32_t id = 0;
     HIPCK(hipMemcpyAsync(&id, d_ids + bad, 4, hipMemcpyDeviceToHost, st));
     HIPCK(hipStreamSynchronize(st));
@@ -1156,6 +1467,12 @@ int ixh_packb8_create(int device, const int8_t *q, const float *scale, int k, in
   return IXH_OK;
 }
 
+int ixh_packb8_set_option(ixh_packed_b8 *b, int option, int64_t value) {
+  if (!b) return fail(IXH_EINVAL, "linalg: nil PackedB8");
+  std::lock_guard<std::mutex> lk(b->mu);
+  return set_tuning(b->tuning, option, value, false);
+}
+
 void ixh_packb8_destroy(ixh_packed_b8 *b) {
   if (!b) return;
   DeviceGuard dg(b->device);
@@ -1163,6 +1480,11 @@ void ixh_packb8_destroy(ixh_packed_b8 *b) {
 }
 
 namespace {
+Tuning pb_tuning(ixh_packed_b8 *b) {
+  std::lock_guard<std::mutex> lk(b->mu);
+  return b->tuning;
+}
+
 // Uploads a [m][k] f32 with rows padded to ld = roundup(k, 4), quantises
 // it into q [m][Kp] (zero padding) and sa [m] on stream st.
 // Host rows a [m][k] into da [m][round_up(k, 4)] (zero padding).
@@ -1259,7 +1581,7 @@ int ixh_matmul8(ixh_packed_b8 *b, float *c, const float *a, int m, int accumulat
   g.ldc = M.n;
   g.n_valid = M.n;
   g.Bk = M.qk.as<int8_t>();
-  run_gemm(accumulate ? EPI_ACCUM : EPI_STORE, g, ts.s);
+  run_gemm(accumulate ? EPI_ACCUM : EPI_STORE, g, pb_tuning(b), ts.s);
   LAUNCHCK("matmul8");
   HIPCK(hipMemcpyAsync(c, dc.p, 4 * (size_t)m * M.n, hipMemcpyDeviceToHost, ts.s));
   HIPCK(hipStreamSynchronize(ts.s));
@@ -1320,7 +1642,7 @@ int matmul8_split(ixh_packed_b8 *b, float *c, const float *a, int m, int accumul
   g.ldc = n;
   g.n_valid = n;
   g.Bk = M.qk.as<int8_t>();
-  run_gemm(accumulate ? EPI_ACCUM : EPI_STORE, g, ts.s);
+  run_gemm(accumulate ? EPI_ACCUM : EPI_STORE, g, pb_tuning(b), ts.s);
   LAUNCHCK("matmul8");
   std::vector<float> w;
   if (nc > 0 || bias) {
@@ -1393,7 +1715,7 @@ int ixh_matmul8_tile(ixh_packed_b8 *b, const float *a, int m, int8_t *aq, float 
     g.ldc = M.n;
     g.n_valid = M.n;
     g.Bk = M.qk.as<int8_t>();
-    run_gemm(EPI_TILE, g, ts.s);
+    run_gemm(EPI_TILE, g, pb_tuning(b), ts.s);
     LAUNCHCK("matmul8_tile");
     HIPCK(hipMemcpyAsync(tile, dt.p, 4 * (size_t)m * M.n, hipMemcpyDeviceToHost, ts.s));
   }
@@ -1506,7 +1828,7 @@ int ixh_ln_matmul8_geglu(ixh_packed_b8 *b, const float *x, int m, const float *g
   ga.lanes = lanes;
   ga.n_gelu = gelu_fma_cols(n / 2, lanes);
   ga.Bk = M.qk.as<int8_t>();
-  run_gemm(EPI_GEGLU, ga, ts.s);
+  run_gemm(EPI_GEGLU, ga, pb_tuning(b), ts.s);
   LAUNCHCK("geglu");
   HIPCK(hipMemcpyAsync(g, dg.p, 4 * (size_t)m * (n / 2), hipMemcpyDeviceToHost, ts.s));
   if (tile) {
@@ -1524,7 +1846,7 @@ int ixh_ln_matmul8_geglu(ixh_packed_b8 *b, const float *x, int m, const float *g
     gt.C = nullptr;
     gt.ldc = n;
     gt.n_valid = n;
-    run_gemm(EPI_TILE, gt, ts.s);
+    run_gemm(EPI_TILE, gt, pb_tuning(b), ts.s);
     LAUNCHCK("geglu_tile");
     HIPCK(hipMemcpyAsync(tile, dt.p, 4 * (size_t)m * n, hipMemcpyDeviceToHost, ts.s));
   }
@@ -1689,7 +2011,9 @@ void batcher_work(ixh_batcher *b) {
       for (int s = 0; s < r->B; s++, k++) offs[k + 1] = offs[k] + (r->offs[s + 1] - r->offs[s]);
     }
     pooled.resize((size_t)B * H);
-    const int rc = encode_host(b->m, ids.data(), offs.data(), B, IXH_OUT_POOLED, pooled.data());
+    Outputs o;
+    o.pooled = pooled.data();
+    const int rc = encode_host(b->m, ids.data(), offs.data(), B, o);
     size_t off = 0;
     for (BatchReq *r : batch) {
       if (rc) {

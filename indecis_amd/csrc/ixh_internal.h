@@ -12,6 +12,20 @@ struct ixh_tokenizer;
 
 namespace ixh {
 
+// Kernel choices of a model or PackedB8 handle (ixh_model_set_option,
+// ixh_packb8_set_option). Each call copies the handle's values once, so a
+// change never reaches a pass already running.
+struct Tuning {
+  int parts = 0;          // streams a large batch is split over: 0 auto, 1..4
+  int pass_tokens = 131072;  // most tokens of one encoder pass
+  int qkv_fused = 1;      // QKV GEMM fused with Attn8.Prepare (sequences <= 512 keys)
+  int qkv_heads = 1;      // heads a workgroup of the fused QKV kernel: 1 or 2
+  int gemm = 0;           // 0: gemm_as for Wi/stores, gemm_i8 residual; 1: gemm_i8 only;
+                          // 2: as 0 with the residual GEMMs on gemm_ws
+  int gemm_tile = 0;      // gemm_i8 tiles: 0 128x128/2 stages, 1 256x128/3, 2 128x128/3
+  int ln_seg = 1;         // LayerNorm lanes 8/16: 1 segment kernel, 0 whole-row LDS kernel
+};
+
 // ---- int8 GEMM ----------------------------------------------------------
 // C = epilogue(A . B^T): A int8 [M][lda] (signed activations, zero
 // padding to Kp), B int8 [Np][ldb] (weights, one row per output channel,
@@ -53,7 +67,7 @@ struct GemmArgs {
   int8_t *qq;
   float *sq;
   float attn_scale;
-  int tile_cfg;  // 0: 128x128 tiles, 2 LDS stages; 1: 256x128, 3; 2: 128x128, 3
+  int tile_cfg;  // gemm_i8: 0: 128x128 tiles, 2 LDS stages; 1: 256x128, 3; 2: 128x128, 3
 };
 
 void launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
@@ -106,6 +120,7 @@ struct RowArgs {
   int8_t *q;               // [M][ldq] quantised result, or nullptr
   int ldq;
   float *sa;               // [M]
+  int seg = 1;             // lanes 8/16: segment kernel (1) or whole-row LDS kernel (0)
 };
 void launch_rownorm(const RowArgs &a, hipStream_t s);
 
@@ -164,8 +179,9 @@ constexpr int kKeyPad = 64;       // key slots of a sequence are padded to this
 // batches whose sequences have at most kQkvSeqMax keys: g as for the
 // EPI_ROPE GEMM (A, sa, B, sb, zc, c128, Kp, rope tables, pos, qq, sq,
 // attn_scale; C unused), a as for launch_attn_prologue (qkv unused);
-// order[B]: the sequences, longest first.
+// order[B]: the sequences, longest first; heads: per workgroup, 1 or 2
+// (2 only for an even head count where the device grants the LDS).
 constexpr int kQkvSeqMax = 512;
-void launch_qkv_attn(const GemmArgs &g, const AttnArgs &a, const int32_t *order, hipStream_t s);
+void launch_qkv_attn(const GemmArgs &g, const AttnArgs &a, const int32_t *order, int heads, hipStream_t s);
 
 }  // namespace ixh

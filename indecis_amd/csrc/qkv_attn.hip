@@ -426,16 +426,15 @@ void launch_nh(const GemmArgs &g, const AttnArgs &a, const int32_t *order, hipSt
 
 }  // namespace
 
-// One head a workgroup; two (1,024 threads) with IXH_QKV_HEADS=2 when the
+// One head a workgroup; two (1,024 threads) on request when the
 // head count is even and the device grants the LDS. Two heads halve the
 // rows brought into LDS per head, but one workgroup then fills a CU and its
 // dequantisation and Attn8.Prepare phases (40% of a workgroup's time) no
 // longer overlap another workgroup's K loop: slower on cfg4 (339 against
 // 315 us a launch).
-void launch_qkv_attn(const GemmArgs &g, const AttnArgs &a, const int32_t *order, hipStream_t s) {
+void launch_qkv_attn(const GemmArgs &g, const AttnArgs &a, const int32_t *order, int heads, hipStream_t s) {
   if (a.B <= 0) return;
-  const char *e = getenv("IXH_QKV_HEADS");
-  const bool pair = e && e[0] == '2' && a.nh % 2 == 0;
+  const bool pair = heads == 2 && a.nh % 2 == 0;
   if (pair && smem_ready<2>()) {
     launch_nh<2>(g, a, order, s);
   } else {

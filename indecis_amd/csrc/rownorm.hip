@@ -618,8 +618,7 @@ void launch_rownorm(const RowArgs &a, hipStream_t s) {
     default: rownorm_seg_kernel<VV, CC, 3><<<groups, 64, 0, s>>>(a); return;            \
     }                                                                                    \
   }
-    const char *se = getenv("IXH_LN_SEG");  // IXH_LN_SEG=0: the whole-row LDS kernel
-    const bool seg = !(se && se[0] == '0');
+    const bool seg = a.seg != 0;  // 0: the whole-row LDS kernel
     IXH_SEG(8, 1) IXH_SEG(8, 2) IXH_SEG(8, 3) IXH_SEG(8, 4)
     IXH_SEG(16, 1) IXH_SEG(16, 2) IXH_SEG(16, 3) IXH_SEG(16, 4)
 #undef IXH_SEG

@@ -30,6 +30,11 @@ class PackedB8:
         _lib.check(_lib.lib().ixh_packb8_create(device, _ptr(q), _ptr(scale), k, n, layout, C.byref(h)))
         self._h = h
 
+    def set_option(self, name, value):
+        """The GEMM kernel choice for calls on this handle
+        (ixh_packb8_set_option): "gemm" or "gemm_tile"."""
+        _lib.check(_lib.lib().ixh_packb8_set_option(self._h, _lib.OPTIONS[name], int(value)))
+
     def close(self):
         if self._h:
             _lib.lib().ixh_packb8_destroy(self._h)

@@ -254,6 +254,51 @@ class Model:
         s = np.ascontiguousarray(sin_t, np.float32)
         _lib.check(self._L.ixh_model_set_rope(self._h, 1 if is_global else 0, _ptr(c), _ptr(s), c.shape[0]))
 
+    def reset_rope(self, is_global):
+        """Back to the library's own RoPE tables (the ropeFor formula)."""
+        _lib.check(self._L.ixh_model_set_rope(self._h, 1 if is_global else 0, None, None, 0))
+
+    def set_option(self, name, value):
+        """A kernel or pass choice (ixh_model_set_option): parts,
+        pass_tokens, qkv_fused, qkv_heads, gemm, gemm_tile, ln_seg.
+        Results never depend on it."""
+        _lib.check(self._L.ixh_model_set_option(self._h, _lib.OPTIONS[name], int(value)))
+
+    def option(self, name):
+        v = C.c_int64(0)
+        _lib.check(self._L.ixh_model_get_option(self._h, _lib.OPTIONS[name], C.byref(v)))
+        return v.value
+
+    def set_heads(self, heads):
+        """The decision heads on the device (ixh_model_set_heads): a list
+        of (w [rows, H], b [rows], per_token) in order; [] removes them."""
+        n = len(heads)
+        ws = [np.ascontiguousarray(w, np.float32) for w, _, _ in heads]
+        bs = [np.ascontiguousarray(b, np.float32) for _, b, _ in heads]
+        rows = np.array([w.shape[0] for w in ws] or [0], np.int32)
+        tok = np.array([1 if t else 0 for _, _, t in heads] or [0], np.int32)
+        wp = (C.c_void_p * max(n, 1))(*[w.ctypes.data for w in ws])
+        bp = (C.c_void_p * max(n, 1))(*[b.ctypes.data for b in bs])
+        _lib.check(self._L.ixh_model_set_heads(self._h, n, _ptr(rows), _ptr(tok), C.cast(wp, C.c_void_p),
+                                               C.cast(bp, C.c_void_p)))
+        self._heads = [(w.shape[0], bool(t)) for (w, _, t) in zip(ws, bs, [h[2] for h in heads])]
+
+    def encode_heads(self, seqs, mean=False, pooled=True, tokens=True):
+        """infer's GPU half (ixh_encode_heads): (pooled_z [B, Rp] or None,
+        token_z [N, Rt] or None), the logits of the pooled-row heads and of
+        the per-token heads, in the order they were set."""
+        heads = getattr(self, "_heads", [])
+        rp = sum(r for r, t in heads if not t)
+        rt = sum(r for r, t in heads if t)
+        ids, offs = _offsets(seqs)
+        B, N = len(seqs), int(offs[-1])
+        zp = np.zeros((max(B, 1), max(rp, 1)), np.float64) if pooled and rp else None
+        zt = np.zeros((max(N, 1), max(rt, 1)), np.float64) if tokens and rt else None
+        _lib.check(self._L.ixh_encode_heads(self._h, _ptr(ids), _ptr(offs), B, 1 if mean else 0,
+                                            _ptr(zp) if zp is not None else None,
+                                            _ptr(zt) if zt is not None else None))
+        return (zp[:B, :rp] if zp is not None else None), (zt[:N, :rt] if zt is not None else None)
+
     def invalidate(self):
         """Invalidate (infer.go:95-100)."""
         _lib.check(self._L.ixh_model_invalidate(self._h))

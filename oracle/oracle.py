@@ -328,6 +328,16 @@ class OracleModel:
         m.rope_cos_local, m.rope_sin_local = ptr(cl, np.float32), ptr(sl, np.float32)
         m.rope_rows = rows
 
+    def set_rope(self, cos_g, sin_g, cos_l, sin_l):
+        """RoPE tables given by a caller ([rows][D/2] each, as ropeFor
+        returns them, model.go:256-277), used as they are for batches of
+        up to `rows` tokens."""
+        m, ptr = self.m, self._ptr
+        rows = min(len(cos_g), len(sin_g), len(cos_l), len(sin_l))
+        m.rope_cos_global, m.rope_sin_global = ptr(cos_g, np.float32), ptr(sin_g, np.float32)
+        m.rope_cos_local, m.rope_sin_local = ptr(cos_l, np.float32), ptr(sin_l, np.float32)
+        m.rope_rows = rows
+
     def encode_tokens(self, seqs):
         """EncodeTokens (infer.go:293-299): [N, H] final states."""
         ids = np.concatenate([np.asarray(s, np.int32) for s in seqs]) if seqs else np.zeros(0, np.int32)

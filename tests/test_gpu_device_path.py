@@ -34,12 +34,12 @@ def _run(gpu, seqs, kind, hidden):
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("split", ["1", "2"])
-def test_device_path_equals_host_path(split, monkeypatch):
-    monkeypatch.setenv("IXH_SPLIT", split)
+@pytest.mark.parametrize("split", [1, 2])
+def test_device_path_equals_host_path(split):
     cfg = small_cfg()
     w = Weights.random(cfg, seed=21)
     gpu = Model(w, lanes=8)
+    gpu.set_option("parts", split)
     rng = np.random.default_rng(21)
     # above the two-part threshold (4,096 tokens) when split = 2
     seqs = ids_uniform_lengths(rng, 40, 1, 300, cfg.vocab)

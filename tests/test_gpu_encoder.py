@@ -3,6 +3,7 @@ against the CPU oracle, through the C ABI, on the BASELINE.json
 configurations (reduced batches where the oracle would take minutes), plus
 the reference's invariants at full size."""
 import concurrent.futures as cf
+import contextlib
 
 import numpy as np
 import pytest
@@ -16,6 +17,20 @@ from oracle import oracle as orc
 pytestmark = pytest.mark.gpu
 
 _models = {}
+
+
+@contextlib.contextmanager
+def options(gpu, **kw):
+    """Sets model options for a block, then restores them (the models are
+    shared between tests)."""
+    old = {k: gpu.option(k) for k in kw}
+    try:
+        for k, v in kw.items():
+            gpu.set_option(k, v)
+        yield
+    finally:
+        for k, v in old.items():
+            gpu.set_option(k, v)
 
 
 def model_pair(cfg, seed=0, emb_format=EMB_F32, lanes=8):
@@ -193,51 +208,52 @@ def test_prologue_edge_lengths(longest):
     assert f32_bits_equal(got, want), mismatch_report(got, want)
 
 
-def test_unfused_qkv_path_exact(monkeypatch):
-    """IXH_QKV_FUSED=0: a batch of short sequences through the QKV GEMM
+def test_unfused_qkv_path_exact():
+    """Option qkv_fused 0: a batch of short sequences through the QKV GEMM
     (float32 K, V) and the separate attention prologue, the path every
     batch with a sequence over 512 keys takes, equals the oracle too."""
-    monkeypatch.setenv("IXH_QKV_FUSED", "0")
     cfg = small_cfg(layers=3)
     w, gpu, ora = model_pair(cfg, seed=23)
     rng = np.random.default_rng(23)
     seqs = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32) for n in (1, 33, 64, 65, 300, 512, 0, 7)]
-    got = gpu.encode_tokens(seqs)
+    with options(gpu, qkv_fused=0):
+        got = gpu.encode_tokens(seqs)
     want, _ = ora.encode_tokens(seqs)
     assert f32_bits_equal(got, want), mismatch_report(got, want)
 
 
-@pytest.mark.parametrize("parts", ["2", "3"])
-def test_split_streams_exact(parts, monkeypatch):
+@pytest.mark.parametrize("parts", [2, 3])
+def test_split_streams_exact(parts):
     """A batch of at least 4,096 tokens runs as parts on as many streams
-    (forward_split; IXH_SPLIT parts, default 2); token states and pooled
-    output equal the oracle's."""
-    monkeypatch.setenv("IXH_SPLIT", parts)
+    (forward_split; option parts, default 2 here); token states and pooled
+    output equal the oracle's, with an empty sequence last (a part of
+    empty sequences only)."""
     cfg = small_cfg(layers=3)
     w, gpu, ora = model_pair(cfg, seed=21)
     rng = np.random.default_rng(21)
-    seqs = ids_uniform_lengths(rng, 40, 64, 256, cfg.vocab)
+    seqs = ids_uniform_lengths(rng, 40, 64, 256, cfg.vocab) + [np.zeros(0, np.int32)]
     assert sum(len(s) for s in seqs) >= 4096
-    got = gpu.encode_tokens(seqs)
+    with options(gpu, parts=parts):
+        got = gpu.encode_tokens(seqs)
+        pooled = gpu.encode_seqs(seqs)
     want, _ = ora.encode_tokens(seqs)
     assert f32_bits_equal(got, want), mismatch_report(got, want)
-    pooled = gpu.encode_seqs(seqs)
     assert f32_bits_equal(pooled, ora.encode_seqs(seqs))
 
 
-@pytest.mark.parametrize("heads_env", ["2", "1"])
-def test_qkv_heads_per_workgroup(heads_env, monkeypatch):
-    """The fused QKV kernel with two heads a workgroup (IXH_QKV_HEADS=2:
+@pytest.mark.parametrize("nheads", [2, 1])
+def test_qkv_heads_per_workgroup(nheads):
+    """The fused QKV kernel with two heads a workgroup (option qkv_heads 2:
     1,024 threads, a 3-stage ring) and with one (the default), at lengths
     around its 32-row blocks and the 256-row slab, up to 512."""
-    monkeypatch.setenv("IXH_QKV_HEADS", heads_env)
     cfg = base_cfg(layers=2)
     w, gpu, ora = model_pair(cfg, seed=31)
     rng = np.random.default_rng(31)
     seqs = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32)
             for n in (1, 31, 32, 33, 255, 256, 257, 300, 511, 512, 0, 64)]
-    got = gpu.encode_tokens(seqs)
+    with options(gpu, qkv_heads=nheads):
+        got = gpu.encode_tokens(seqs)
+        pooled = gpu.encode_seqs(seqs)
     want, _ = ora.encode_tokens(seqs)
     assert f32_bits_equal(got, want), mismatch_report(got, want)
-    pooled = gpu.encode_seqs(seqs)
     assert f32_bits_equal(pooled, ora.encode_seqs(seqs))

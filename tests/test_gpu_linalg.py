@@ -129,20 +129,19 @@ def test_attend8_exact(n, window, lanes):
     assert f32_bits_equal(o, ref), mismatch_report(o, ref)
 
 
-@pytest.mark.parametrize("tile_cfg", ["0", "1", "2"])
-def test_gemm_tile_configs(tile_cfg, monkeypatch):
-    """The gemm_i8 kernel alone (IXH_GEMM_AS=0, IXH_GEMM_WS=0) in its default 128x128 and
+@pytest.mark.parametrize("tile_cfg", [0, 1, 2])
+def test_gemm_tile_configs(tile_cfg):
+    """The gemm_i8 kernel alone (option gemm 1) in its default 128x128 and
     its 256x128 / 3-stage and 128x128 / 3-stage tile configurations
-    (IXH_GEMM_TILE) gives the oracle's reference tile and floats, on ragged
-    shapes that leave partial M tiles and padded N and K."""
-    monkeypatch.setenv("IXH_GEMM_AS", "0")
-    monkeypatch.setenv("IXH_GEMM_WS", "0")
-    monkeypatch.setenv("IXH_GEMM_TILE", tile_cfg)
-    rng = np.random.default_rng(int(tile_cfg))
+    (option gemm_tile) gives the oracle's reference tile and floats, on
+    ragged shapes that leave partial M tiles and padded N and K."""
+    rng = np.random.default_rng(tile_cfg)
     for m, k, n in [(7, 384, 1152), (257, 70, 40), (300, 1152, 768), (1000, 768, 2304)]:
         a = rng.standard_normal((m, k)).astype(np.float32)
         q, s = _weights(rng, n, k)
         b = linalg.PackedB8(q, s)
+        b.set_option("gemm", 1)
+        b.set_option("gemm_tile", tile_cfg)
         aq, sa, tile = linalg.matmul8_tile(a, b)
         aq_ref, sa_ref = orc.quantize_rows(a)
         assert np.array_equal(tile, orc.matmul8_tile(aq_ref, q))
@@ -155,6 +154,8 @@ def test_gemm_tile_configs(tile_cfg, monkeypatch):
     cfg = small_cfg()
     w = Weights.random(cfg, seed=5)
     gpu, ora = Model(w, lanes=8), orc.OracleModel(w, lanes=8)
+    gpu.set_option("gemm", 1)
+    gpu.set_option("gemm_tile", tile_cfg)
     seqs = ids_uniform_lengths(rng, 5, 1, 300, cfg.vocab)
     got = gpu.encode_tokens(seqs)
     want, _ = ora.encode_tokens(seqs)
@@ -188,16 +189,15 @@ def test_gemm_as_exact(m, k, n, kind):
         assert f32_bits_equal(got, ref), mismatch_report(got, ref)
 
 
-@pytest.mark.parametrize("as_on,ws_on", [("0", "0"), ("0", "1"), ("1", "1")])
-def test_encoder_gemm_kernel_choices(as_on, ws_on, monkeypatch):
-    """IXH_GEMM_AS / IXH_GEMM_WS: the whole encoder on gemm_i8 alone (Wi +
-    GeGLU and the residual GEMMs included), or with the opt-in
-    warp-specialised kernel for the residual GEMMs, equals the oracle too."""
-    monkeypatch.setenv("IXH_GEMM_AS", as_on)
-    monkeypatch.setenv("IXH_GEMM_WS", ws_on)
+@pytest.mark.parametrize("gemm", [1, 2])
+def test_encoder_gemm_kernel_choices(gemm):
+    """Option gemm: the whole encoder on gemm_i8 alone (1: Wi + GeGLU and
+    the residual GEMMs included), or with the warp-specialised kernel for
+    the residual GEMMs (2), equals the oracle too."""
     cfg = small_cfg()
     w = Weights.random(cfg, seed=9)
     gpu, ora = Model(w, lanes=8), orc.OracleModel(w, lanes=8)
+    gpu.set_option("gemm", gemm)
     rng = np.random.default_rng(9)
     seqs = ids_uniform_lengths(rng, 5, 1, 300, cfg.vocab)
     got = gpu.encode_tokens(seqs)
@@ -209,20 +209,20 @@ def test_encoder_gemm_kernel_choices(as_on, ws_on, monkeypatch):
 @pytest.mark.parametrize("kind", ["random", "max"])
 @pytest.mark.parametrize("m,k,n", [(1, 768, 256), (64, 256, 256), (65, 512, 768), (700, 1152, 768),
                                    (3001, 768, 768), (4100, 1152, 768)])
-def test_gemm_ws_accumulate_exact(m, k, n, kind, monkeypatch):
-    """The warp-specialised GEMM (gemm_ws.hip, IXH_GEMM_WS=1: MatMul8N with
+def test_gemm_ws_accumulate_exact(m, k, n, kind):
+    """The warp-specialised GEMM (gemm_ws.hip, option gemm 2: MatMul8N with
     accumulate, int8.go:89-155, as the residual GEMMs run it) adds the oracle's
     floats to C bit for bit: partial 64-row M-blocks, one-row inputs, runs
     of units that cross M-blocks, all weights 127. Each shape runs three
     times on the same inputs: the MFMA and epilogue waves hand blocks over
     through LDS, and every call must give the same bits."""
-    monkeypatch.setenv("IXH_GEMM_WS", "1")
     rng = np.random.default_rng(m * 17 + k + 3 * n)
     a = (rng.standard_normal((m, k)) * 3).astype(np.float32)
     if kind == "max":
         a[:] = np.abs(a) + 1
     q, s = _weights(rng, n, k, kind)
     b = linalg.PackedB8(q, s)
+    b.set_option("gemm", 2)
     colsum = q.astype(np.int32).sum(axis=1).astype(np.int32)
     c0 = rng.standard_normal((m, n)).astype(np.float32)
     ref = orc.matmul8(a, q, s, colsum, c=c0, accumulate=True)
