@@ -510,6 +510,76 @@ void ixo_attend8(float *o, int ldo, const float *q, const float *k,
   free(s); free(pq);
 }
 
+/* Attn8.Attend (attention8.go:298-376) blocked as the reference blocks it:
+ * queries [i0, i1) in blocks of 48 (AttnBlock, :26); a block's scores over
+ * whole 16-key panels [c0, c1) covering its windows (:313-316), the
+ * padding keys of the last panel scoring 0; per row the valid keys
+ * (:345-348), ExpShift over them, QuantizeRowU8 and 1/sum P (:349-355);
+ * P.V over the block's panels, the other keys' weights 0 (:358-373). Row i
+ * goes to o[(i - i0)*ldo]. Test infrastructure: it checks the per-query
+ * restatement ixo_attend8 (TestAttn8Ranges). plant != 0 plants a mistake
+ * the tests must catch: 1 an exclusive window bound (|i - j| < window),
+ * 2 the weights normalised by 1/(255 * sum e) instead of 1/sum P. */
+void ixo_attend8_blocked(float *o, int ldo, const float *q, const float *k,
+                         const float *v, int ld, int n, int D, int i0, int i1,
+                         int window, float scale, int lanes, int plant) {
+  if (n <= 0 || i0 >= i1) return;
+  enum { BLOCK = 48, PANEL = 16 };
+  const int npad = (n + PANEL - 1) / PANEL * PANEL;
+  int8_t *qq = (int8_t *)malloc((size_t)n * D);
+  int8_t *kq = (int8_t *)calloc((size_t)npad * D, 1);
+  int8_t *vq = (int8_t *)calloc((size_t)npad * D, 1);
+  float *sq = (float *)malloc(sizeof(float) * n);
+  float *ks = (float *)calloc(npad, sizeof(float));
+  float *vs = (float *)malloc(sizeof(float) * D);
+  float *mean = (float *)malloc(sizeof(float) * D);
+  ixo_attn_prepare(q, k, v, ld, n, D, scale, qq, sq, kq, ks, vq, vs, mean);
+  float *s = (float *)malloc(sizeof(float) * BLOCK * npad);
+  int32_t *p = (int32_t *)malloc(sizeof(int32_t) * BLOCK * npad);
+  float sp[BLOCK];
+  for (int b0 = i0; b0 < i1; b0 += BLOCK) {
+    const int b1 = b0 + BLOCK < i1 ? b0 + BLOCK : i1;
+    int c0 = 0, c1 = npad;
+    if (window >= 0) {
+      c0 = (b0 - window > 0 ? b0 - window : 0) / PANEL * PANEL;
+      int e = (b1 - 1 + window + 1 + PANEL - 1) / PANEL * PANEL;
+      c1 = e < npad ? e : npad;
+    }
+    const int W = c1 - c0;
+    for (int i = b0; i < b1; i++)
+      for (int j = c0; j < c1; j++) {
+        int32_t acc = dot_i8(qq + (size_t)i * D, kq + (size_t)j * D, D);
+        s[(i - b0) * W + j - c0] = ((float)acc * ks[j]) * sq[i];
+      }
+    for (int i = b0; i < b1; i++) {
+      float *row = s + (size_t)(i - b0) * W;
+      int32_t *prow = p + (size_t)(i - b0) * W;
+      int cs = 0, ce = (n < c1 ? n : c1) - c0;
+      if (window >= 0) {
+        const int w = plant == 1 ? window - 1 : window;
+        cs = i - w - c0 > 0 ? i - w - c0 : 0;
+        ce = (i + w + 1 < n ? i + w + 1 : n) - c0;
+      }
+      float mx = -INFINITY;
+      for (int j = cs; j < ce; j++) mx = fmax32(mx, row[j]);
+      const float esum = ixo_exp_shift(row + cs, ce - cs, mx, lanes);
+      int32_t sum = 0;
+      for (int j = 0; j < W; j++) {
+        prow[j] = j >= cs && j < ce ? (int32_t)ixo_round_half_even(row[j] * 255.0f) : 0;
+        sum += prow[j];
+      }
+      sp[i - b0] = plant == 2 ? 1.0f / (255.0f * esum) : 1.0f / (float)sum;
+    }
+    for (int i = b0; i < b1; i++)
+      for (int d = 0; d < D; d++) {
+        int32_t tile = 0;
+        for (int j = 0; j < W; j++) tile += p[(size_t)(i - b0) * W + j] * (int32_t)vq[(size_t)(c0 + j) * D + d];
+        o[(size_t)(i - i0) * ldo + d] = (((float)tile - 0.0f) * vs[d]) * sp[i - b0];
+      }
+  }
+  free(qq); free(kq); free(vq); free(sq); free(ks); free(vs); free(mean); free(s); free(p);
+}
+
 /* ---- encoder ------------------------------------------------------------ */
 
 static uint32_t u16_le(const uint16_t *p) { return (uint32_t)*p; }
@@ -524,7 +594,9 @@ void ixo_embed_row(const ixo_model *m, int32_t id, float *dst) {
     return;
   }
   case IXO_EMB_BF16: {
-    for (int e = 0; e < m->emb_n_exact; e++)
+    /* newMappedEmbeddings fills a map in row order (embeddings.go:38-44):
+     * of two rows for one id, the later one is read */
+    for (int e = m->emb_n_exact - 1; e >= 0; e--)
       if (m->emb_exact_ids[e] == id) {
         memcpy(dst, m->emb_exact_rows + (size_t)e * H, sizeof(float) * H);
         return;

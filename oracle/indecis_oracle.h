@@ -109,6 +109,13 @@ void ixo_attend8(float *o, int ldo, const float *q, const float *k,
                  const float *v, int ld, int n, int D, int window,
                  float scale, int lanes);
 
+/* Attn8.Attend blocked as the reference blocks it (48 queries, 16-key
+ * panels), queries [i0, i1) into o[(i - i0)*ldo]; plant 1 or 2 plants a
+ * mistake (exclusive window bound; 1/(255 sum e) normalisation). */
+void ixo_attend8_blocked(float *o, int ldo, const float *q, const float *k,
+                         const float *v, int ld, int n, int D, int i0, int i1,
+                         int window, float scale, int lanes, int plant);
+
 /* Attn8.Prepare outputs (attention8.go:203-280), for checking the GPU
  * attention prologue: qq [n][D] signed, sq [n]; kq [n][D] signed
  * (centred), ks [n]; vq [n][D] signed, vs [D]; kmean [D]. */

@@ -82,11 +82,14 @@ def lib():
         L.ixo_rope.argtypes = [f32p, f32p, f32p, C.c_int]
         L.ixo_attend8.argtypes = [f32p, C.c_int, f32p, f32p, f32p, C.c_int, C.c_int,
                                   C.c_int, C.c_int, C.c_float, C.c_int]
+        L.ixo_attend8_blocked.argtypes = [C.c_void_p, C.c_int, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int,
+                                          C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, C.c_int]
         L.ixo_attn_prepare.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_float,
                                        i8p, f32p, i8p, f32p, i8p, f32p, f32p]
         L.ixo_encode.argtypes = [C.POINTER(IxoModel), i32p, i32p, C.c_int, f32p]
         L.ixo_encode.restype = C.c_int
         L.ixo_pool.argtypes = [f32p, i32p, C.c_int, C.c_int, C.c_int, f32p]
+        L.ixo_embed_row.argtypes = [C.POINTER(IxoModel), C.c_int32, f32p]
         L.ixo_head_logits.argtypes = [f32p, C.c_int, C.c_int, f32p, f32p, C.c_int, f64p]
         _lib = L
     return _lib
@@ -263,6 +266,16 @@ def attend8(q, k, v, window=-1, scale=0.125, lanes=8):
     return o
 
 
+def attend8_blocked(o, off, ldo, q, k, v, i0, i1, window=-1, scale=0.125, lanes=8, plant=0):
+    """Attn8.Attend as the reference blocks it, queries [i0, i1) written to
+    the float32 array o from element `off` on, rows ldo apart."""
+    q, k, v = (_c(t, np.float32) for t in (q, k, v))
+    n, D = q.shape
+    assert o.dtype == np.float32 and o.flags.c_contiguous
+    assert off + (i1 - i0 - 1) * ldo + D <= o.size
+    lib().ixo_attend8_blocked(o.ctypes.data + 4 * off, ldo, q, k, v, D, n, D, i0, i1, window, scale, lanes, plant)
+
+
 def attn_prepare(q, k, v, scale=0.125):
     q, k, v = (_c(t, np.float32) for t in (q, k, v))
     n, D = q.shape
@@ -337,6 +350,12 @@ class OracleModel:
         m.rope_cos_global, m.rope_sin_global = ptr(cos_g, np.float32), ptr(sin_g, np.float32)
         m.rope_cos_local, m.rope_sin_local = ptr(cos_l, np.float32), ptr(sin_l, np.float32)
         m.rope_rows = rows
+
+    def embed_row(self, id_):
+        """embRow (infer.go:52-59, embeddings.go:48-68): the table row of id."""
+        out = np.zeros(self.w.cfg.hidden, np.float32)
+        lib().ixo_embed_row(C.byref(self.m), int(id_), out)
+        return out
 
     def encode_tokens(self, seqs):
         """EncodeTokens (infer.go:293-299): [N, H] final states."""

@@ -254,3 +254,21 @@ def test_option_values_checked():
     gpu.set_option("parts", 2)
     assert gpu.option("parts") == 2
     gpu.close()
+
+
+def test_bf16_exact_rows_later_wins():
+    """A bf16 table whose exact rows name one id twice: the later row is
+    read (newMappedEmbeddings fills a map in row order, embeddings.go:38-44),
+    on the GPU as in the oracle."""
+    from indecis_amd.modernbert import EMB_BF16
+    cfg = small_cfg(layers=1)
+    w = Weights.random(cfg, seed=48, emb_format=EMB_BF16)
+    rng = np.random.default_rng(48)
+    w.emb_exact_ids = np.array([5, 9, 5], np.int32)
+    w.emb_exact_rows = rng.standard_normal((3, cfg.hidden)).astype(np.float32)
+    gpu, ora = Model(w, lanes=8), orc.OracleModel(w, lanes=8)
+    seqs = [np.array([5, 9, 5, 11], np.int32), rng.integers(0, cfg.vocab, size=30, dtype=np.int32)]
+    got = gpu.encode_tokens(seqs)
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+    gpu.close()

@@ -11,7 +11,7 @@ import pytest
 
 import float_reference as fref
 from helpers import small_cfg, ids_uniform_lengths
-from indecis_amd.modernbert import Weights, pack_b8 as host_pack_b8
+from indecis_amd.modernbert import EMB_BF16, EMB_F32, EMB_I8, Weights, pack_b8 as host_pack_b8
 from oracle import oracle as orc
 
 
@@ -482,19 +482,180 @@ def test_attn_prepare_invariants():
     assert np.array_equal(p["sq"], (qs * np.float32(0.125)).astype(np.float32))
 
 
-def test_attend8_blocks_independent():
-    """TestAttn8Ranges (attention8_test.go:87-114): a query's output does not
-    depend on which other queries share its block — a prefix of the keys
-    gives the same rows when the window keeps them out of reach."""
-    rng = np.random.default_rng(12)
-    n, D, W = 259, 64, 8
+def _attend_fns():
+    """The per-query restatement, and the reference's blocked form."""
+    def per_query(q, k, v, window, lanes=8):
+        return orc.attend8(q, k, v, window, 0.125, lanes)
+
+    def blocked(plant):
+        def f(q, k, v, window, lanes=8):
+            n, D = q.shape
+            o = np.zeros((n, D), np.float32)
+            orc.attend8_blocked(o, 0, D, q, k, v, 0, n, window, 0.125, lanes, plant)
+            return o
+        return f
+    return per_query, blocked
+
+
+def test_attn8_ranges():
+    """TestAttn8Ranges (attention8_test.go:87-114): ranges of 48 queries
+    computed apart by the reference's blocked Attend (16-key panels, the
+    block's window span), into a wider output, give exactly the per-query
+    restatement's whole attention; n = 259, windows -1 and 64, every lane
+    width. A blocked form with an exclusive window bound (plant 1) or the
+    1/(255 sum e) normalisation (plant 2) is caught."""
+    rng = np.random.default_rng(34)
+    n, D, ldo = 259, 64, 64 * 3
     q, k, v = (rng.standard_normal((n, D)).astype(np.float32) for _ in range(3))
-    full = orc.attend8(q, k, v, W, 0.125, 8)
-    assert np.all(np.isfinite(full))
-    # K's mean and V's scales depend on every key: identical inputs, shuffled
-    # block boundaries, must give identical bits
-    again = orc.attend8(q, k, v, W, 0.125, 8)
-    assert np.array_equal(full, again)
+    for window in (-1, 64):
+        for lanes in (0, 4, 8, 16):
+            want = orc.attend8(q, k, v, window, 0.125, lanes)
+            o = np.zeros(n * ldo, np.float32)
+            for i0 in range(0, n, 48):
+                orc.attend8_blocked(o, i0 * ldo + D, ldo, q, k, v, i0, min(n, i0 + 48), window, 0.125, lanes)
+            got = o.reshape(n, ldo)[:, D:2 * D]
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (window, lanes)
+    _, blocked = _attend_fns()
+    assert not np.array_equal(blocked(1)(q, k, v, 64), orc.attend8(q, k, v, 64, 0.125, 8))
+    assert not np.array_equal(blocked(2)(q, k, v, -1), orc.attend8(q, k, v, -1, 0.125, 8))
+
+
+def _vquant(v):
+    """Attn8.Prepare's V (attention8.go:180-198): per dimension vs =
+    max|v|/127, q = RNE(v * (1/vs)) in float32."""
+    vs = (np.abs(v).max(axis=0) / np.float32(127)).astype(np.float32)
+    inv = (np.float32(1) / vs).astype(np.float32)
+    return np.rint((v * inv).astype(np.float32)).astype(np.int32), vs
+
+
+def _deq(tile, vs, psum):
+    """O = ((f32(tile) - 0) * vs) * f32(1/sum P) in float32."""
+    sp = np.float32(1) / np.float32(psum)
+    return ((tile.astype(np.float32) * vs).astype(np.float32) * sp).astype(np.float32)
+
+
+def _check_single_key(fn):
+    rng = np.random.default_rng(51)
+    q, k, v = (rng.standard_normal((1, 64)).astype(np.float32) for _ in range(3))
+    o = fn(q, k, v, -1)[0]
+    qv, vs = _vquant(v)
+    assert np.all(np.abs(qv) == 127)
+    want = _deq(255 * qv[0], vs, 255)  # P = [255], sum P = 255
+    return np.array_equal(o.view(np.uint32), want.view(np.uint32)) and np.allclose(o, v[0], rtol=1e-6)
+
+
+def _check_two_keys(fn):
+    """q = [1, 0, ...], keys [c, 0, ...] and [-c, 0, ...] (mean 0): scores
+    s0 = -s1, s0 - s1 = ln(255/127.3) nearly; P = [255, 127], O = (255 qv0
+    + 127 qv1) vs / 382, not / (255 (1 + e1)) = 382.3."""
+    rng = np.random.default_rng(52)
+    q = np.zeros((2, 64), np.float32)
+    q[:, 0] = 1.0
+    c = np.float32(2.779)
+    k = np.zeros((2, 64), np.float32)
+    k[0, 0], k[1, 0] = c, -c
+    v = rng.standard_normal((2, 64)).astype(np.float32)
+    s0 = 0.125 * float(c)  # float64 value of the score, 127*127 scaled
+    p1 = 255 * np.exp(-2 * s0)
+    assert abs(p1 - round(p1)) < 0.4 and round(p1) == 127  # far from a rounding tie
+    qv, vs = _vquant(v)
+    want = _deq(255 * qv[0] + 127 * qv[1], vs, 382)
+    o = fn(q, k, v, -1)
+    alt = _deq(255 * qv[0] + 127 * qv[1], vs, np.float32(255) * np.float32(1 + np.exp(-2 * s0)))
+    assert not np.array_equal(want, alt)
+    return all(np.array_equal(r.view(np.uint32), want.view(np.uint32)) for r in o)
+
+
+def _check_window_edge(fn):
+    """Window 4, one dominant key j* = 20 (every other key scores far
+    below it): queries at distance exactly 4 read only key j*; at distance
+    5 their window is all equal scores, P = 255 each."""
+    rng = np.random.default_rng(53)
+    n, js, w = 40, 20, 4
+    q = np.zeros((n, 64), np.float32)
+    q[:, 0] = 1.0
+    k = np.zeros((n, 64), np.float32)
+    k[js, 0] = 400.0
+    v = rng.standard_normal((n, 64)).astype(np.float32)
+    qv, vs = _vquant(v)
+    o = fn(q, k, v, w)
+    ok = True
+    for i in (js - w, js + w):
+        want = _deq(255 * qv[js], vs, 255)
+        ok &= np.array_equal(o[i].view(np.uint32), want.view(np.uint32))
+    for i in (js - w - 1, js + w + 1):
+        lo, hi = max(0, i - w), min(n, i + w + 1)
+        want = _deq(255 * qv[lo:hi].sum(axis=0), vs, 255 * (hi - lo))
+        ok &= np.array_equal(o[i].view(np.uint32), want.view(np.uint32))
+    return ok
+
+
+def test_attend8_closed_forms():
+    """Attend8 (attention8.go:298-376) where P is known exactly: one key
+    (P = [255]), two keys with P = [255, 127] (normalised by 1/sum P, not
+    1/(255 sum e)), and a window of 4 around a dominant key (the bound
+    |i - j| <= window is inclusive). The per-query restatement and the
+    blocked one pass; planted mistakes fail: an exclusive window bound
+    (plant 1) fails the window case, the 1/(255 sum e) normalisation
+    (plant 2) the two-key case."""
+    per_query, blocked = _attend_fns()
+    for fn in (per_query, blocked(0)):
+        assert _check_single_key(fn)
+        assert _check_two_keys(fn)
+        assert _check_window_edge(fn)
+    assert not _check_window_edge(blocked(1))
+    assert not _check_two_keys(blocked(2))
+
+
+def test_embedding_rows_pinned():
+    """embRow / mappedEmbeddings.Row (infer.go:52-59, embeddings.go:48-68)
+    against the formats' definitions, computed here without the oracle:
+    bf16 is the high half of a float32 (bits << 16, sign and all); an exact
+    row overrides its id, the later of two rows for one id winning (the
+    map is filled in row order, embeddings.go:38-44); int8 rows are
+    float32(int8) * row scale, negative entries included. The encoder on
+    a bf16 (int8) table equals the encoder on the float32 table of those
+    values bit for bit."""
+    cfg = small_cfg(layers=1)
+    w = Weights.random(cfg, seed=61, emb_format=EMB_BF16)
+    rng = np.random.default_rng(61)
+    H = cfg.hidden
+    ids = np.array([5, 9, 5, 70], np.int32)
+    rows = rng.standard_normal((4, H)).astype(np.float32)
+    w.emb_exact_ids, w.emb_exact_rows = ids, rows
+    assert np.any(w.emb_bf16 >= 0x8000)  # negative values present
+    widened = (w.emb_bf16.astype(np.uint32) << 16).view(np.float32)
+    table = widened.copy()
+    for e, i in enumerate(ids):
+        table[i] = rows[e]  # later rows win
+    ora = orc.OracleModel(w, lanes=8)
+    for i in (0, 5, 9, 70, 123, cfg.vocab - 1):
+        assert np.array_equal(ora.embed_row(i).view(np.uint32), table[i].view(np.uint32)), i
+    assert np.array_equal(ora.embed_row(5), rows[2]) and not np.array_equal(rows[0], rows[2])
+    w32 = Weights.random(cfg, seed=61)
+    for name in ("wqkv_q", "wqkv_s", "wo_q", "wo_s", "wi_q", "wi_s", "womlp_q", "womlp_s",
+                 "attn_norm", "mlp_norm", "emb_norm", "final_norm"):
+        setattr(w32, name, getattr(w, name))
+    w32.set_embeddings(table, EMB_F32)
+    seqs = [np.array([5, 9, 70, 3, 5], np.int32), rng.integers(0, cfg.vocab, size=50, dtype=np.int32)]
+    a, _ = ora.encode_tokens(seqs)
+    b, _ = orc.OracleModel(w32, lanes=8).encode_tokens(seqs)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # int8 table with a scale per row
+    w8 = Weights.random(cfg, seed=62, emb_format=EMB_I8)
+    assert np.any(w8.emb_i8 < 0)
+    t8 = (w8.emb_i8.astype(np.float32) * w8.emb_i8_scale[:, None]).astype(np.float32)
+    o8 = orc.OracleModel(w8, lanes=8)
+    for i in (0, 7, cfg.vocab - 1):
+        assert np.array_equal(o8.embed_row(i).view(np.uint32), t8[i].view(np.uint32)), i
+    w8f = Weights.random(cfg, seed=62)
+    for name in ("wqkv_q", "wqkv_s", "wo_q", "wo_s", "wi_q", "wi_s", "womlp_q", "womlp_s",
+                 "attn_norm", "mlp_norm", "emb_norm", "final_norm"):
+        setattr(w8f, name, getattr(w8, name))
+    w8f.set_embeddings(t8, EMB_F32)
+    a, _ = o8.encode_tokens(seqs)
+    b, _ = orc.OracleModel(w8f, lanes=8).encode_tokens(seqs)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 # ---- encoder ------------------------------------------------------------------
