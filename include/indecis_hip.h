@@ -305,6 +305,21 @@ int ixh_packb8_set_option(ixh_packed_b8 *b, int option, int64_t value);
 int ixh_matmul8(ixh_packed_b8 *b, float *c, const float *a, int m,
                 int accumulate);
 
+/* MatMul8N on device buffers that allocates nothing. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, serving loops or harnesses that forbid hipMalloc). d_a [m][lda]
+ * and d_c [m][ldc] float32 in the memory of b's GPU, 16-byte aligned;
+ * k % 4 == 0, lda >= k and a multiple of 4, ldc >= n. The quantised
+ * activations and their scales go to a fixed scratch array of 32 MiB per
+ * GPU (module memory, held until the process ends): m * (round_up(k, 64) +
+ * 4) bytes (plus alignment) must fit, else IXH_EINVAL with the limit. The
+ * work is queued on `stream` (a hipStream_t; NULL: the null stream) and
+ * the call returns without waiting. Every call on a GPU shares that GPU's
+ * scratch: calls that overlap on one GPU race, so serialise them (one
+ * stream, or wait between calls). */
+int ixh_matmul8_noalloc(ixh_packed_b8 *b, float *d_c, int ldc, const float *d_a,
+                        int lda, int m, int accumulate, void *stream);
+
 /* MatMul8Outliers (linalg/int8.go:272-349), the LLM.int8() decomposition:
  * the input channels whose column max |a| exceeds ratio times the mean of
  * the column maxima (the 32 largest when more) are zeroed in a copy of a,

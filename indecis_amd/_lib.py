@@ -26,7 +26,7 @@ EXPORTS = [
     "ixh_model_set_profiling", "ixh_model_set_profile_filter", "ixh_model_profile",
     "ixh_check_exp255", "ixh_batcher_create", "ixh_batcher_encode", "ixh_batcher_stats",
     "ixh_batcher_destroy", "ixh_model_set_option", "ixh_model_get_option", "ixh_packb8_set_option",
-    "ixh_model_set_heads", "ixh_encode_heads",
+    "ixh_model_set_heads", "ixh_encode_heads", "ixh_matmul8_noalloc",
 ]
 
 IXH_OK, IXH_EINVAL, IXH_ERANGE, IXH_ESTATE, IXH_EHIP, IXH_ENOMEM, IXH_EFORMAT = range(7)
@@ -125,6 +125,7 @@ def lib():
         "ixh_packb8_set_option": [vp, C.c_int, C.c_int64],
         "ixh_model_set_heads": [vp, C.c_int, vp, vp, vp, vp],
         "ixh_encode_heads": [vp, vp, vp, C.c_int, C.c_int, vp, vp],
+        "ixh_matmul8_noalloc": [vp, vp, C.c_int, vp, C.c_int, C.c_int, C.c_int, vp],
     }
     for name, args in sig.items():
         f = getattr(L, name)

@@ -1067,6 +1067,33 @@ int encode_host(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, co
 
 }  // namespace
 
+// ---- fixed scratch of the allocation-free MatMul8N (ixh_matmul8_noalloc) --
+// The quantised activations and row scales of one call. Module memory: each
+// GPU the library runs on holds its own copy until the process ends. Host
+// code never takes the array's name as an address: scratch_ptr() resolves
+// the device's copy once, with that device current.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) int8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[64];  // per device ordinal
+
+int scratch_ptr(int dev, void **out) {
+  if (dev < 0 || dev >= 64) return fail(IXH_EINVAL, "linalg: hip: device %d", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(IXH_EHIP, "linalg: hip: %s (hipGetSymbolAddress scratch)", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return IXH_OK;
+}
+}  // namespace
+
 namespace ixh {
 int set_error(int code, const char *msg) {
   g_err = msg;
@@ -1454,6 +1481,9 @@ int ixh_packb8_create(int device, const int8_t *q, const float *scale, int k, in
   if (layout != IXH_LAYOUT_ROWS && layout != IXH_LAYOUT_PANELS)
     return fail(IXH_EINVAL, "linalg: PackB8: layout %d", layout);
   DEVGUARD(device);
+  void *sp = nullptr;
+  int src = scratch_ptr(device, &sp);  // set-up: resolve the device's scratch copy now
+  if (src) return src;
   auto *b = new ixh_packed_b8();
   b->device = device;
   b->rows = to_rows(q, k, n, layout);
@@ -1585,6 +1615,55 @@ int ixh_matmul8(ixh_packed_b8 *b, float *c, const float *a, int m, int accumulat
   LAUNCHCK("matmul8");
   HIPCK(hipMemcpyAsync(c, dc.p, 4 * (size_t)m * M.n, hipMemcpyDeviceToHost, ts.s));
   HIPCK(hipStreamSynchronize(ts.s));
+  return IXH_OK;
+}
+
+int ixh_matmul8_noalloc(ixh_packed_b8 *b, float *d_c, int ldc, const float *d_a, int lda, int m,
+                        int accumulate, void *stream) {
+  if (!b || m < 0 || (m > 0 && (!d_c || !d_a))) return fail(IXH_EINVAL, "linalg: MatMul8: slice too short");
+  const Mat &M = b->mat;
+  if (M.k % 4 != 0 || lda < M.k || lda % 4 != 0 || ldc < M.n || ((uintptr_t)d_a & 15) ||
+      ((uintptr_t)d_c & 15))
+    return fail(IXH_EINVAL,
+                "linalg: hip: MatMul8 without allocation needs k %% 4 == 0, lda >= k and a multiple of "
+                "4, ldc >= n, 16-byte aligned buffers (k %d, n %d, lda %d, ldc %d)",
+                M.k, M.n, lda, ldc);
+  if (m == 0) return IXH_OK;
+  const size_t qbytes = round_up((size_t)m * M.kp, 256);
+  const size_t need = qbytes + 4 * (size_t)m;
+  if (need > kNoAllocScratchBytes)
+    return fail(IXH_EINVAL,
+                "linalg: hip: MatMul8 without allocation: %d rows of depth %d need %zu bytes of "
+                "scratch, over its %zu (at most %zu rows)",
+                m, M.kp, need, kNoAllocScratchBytes, (kNoAllocScratchBytes - 256) / (M.kp + 4));
+  DEVGUARD(b->device);
+  void *sp = nullptr;
+  int rc;
+  if ((rc = scratch_ptr(b->device, &sp))) return rc;
+  int8_t *dq = (int8_t *)sp;
+  float *dsa = (float *)((char *)sp + qbytes);
+  hipStream_t st = (hipStream_t)stream;
+  // quantizeA (int8.go:160-191) into the scratch: rows padded with zeros to Kp
+  launch_quant_rows(d_a, lda, m, M.k, dq, M.kp, dsa, st);
+  LAUNCHCK("quant_rows");
+  GemmArgs g{};
+  g.A = dq;
+  g.lda = M.kp;
+  g.B = M.q.as<int8_t>();
+  g.ldb = M.kp;
+  g.Bk = M.qk.as<int8_t>();
+  g.M = m;
+  g.Np = M.np;
+  g.Kp = M.kp;
+  g.sa = dsa;
+  g.sb = M.sb.as<float>();
+  g.zc = M.zc.as<float>();
+  g.c128 = M.c128.as<int32_t>();
+  g.C = d_c;
+  g.ldc = ldc;
+  g.n_valid = M.n;
+  run_gemm(accumulate ? EPI_ACCUM : EPI_STORE, g, pb_tuning(b), st);
+  LAUNCHCK("matmul8");
   return IXH_OK;
 }
 
