@@ -196,6 +196,8 @@ enum {
                               1: the tiled GEMM only; 2: as 0, residual GEMMs warp-specialised */
   IXH_OPT_GEMM_TILE = 5,   /* tiled GEMM: 0 (default) 128x128 2 stages, 1 256x128 3, 2 128x128 3 */
   IXH_OPT_LN_SEG = 6,      /* LayerNorm at lanes 8/16: 1 (default) segment kernel, 0 whole-row */
+  IXH_OPT_FUSE_RES = 7,    /* 1 (default): Wo and WoMLP fused with the quantisation of their
+                              input and the next LayerNorm + quantisation; 0: separate kernels */
 };
 int ixh_model_set_option(ixh_model *m, int option, int64_t value);
 int ixh_model_get_option(ixh_model *m, int option, int64_t *value);

@@ -355,6 +355,10 @@ int set_tuning(Tuning &t, int option, int64_t v, bool model_opts) {
     if (v != 0 && v != 1) return bad();
     t.ln_seg = (int)v;
     return IXH_OK;
+  case IXH_OPT_FUSE_RES:
+    if (v != 0 && v != 1) return bad();
+    t.fuse_res = (int)v;
+    return IXH_OK;
   default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
   }
 }
@@ -368,6 +372,7 @@ int get_tuning(const Tuning &t, int option, int64_t *v) {
   case IXH_OPT_GEMM: *v = t.gemm; return IXH_OK;
   case IXH_OPT_GEMM_TILE: *v = t.gemm_tile; return IXH_OK;
   case IXH_OPT_LN_SEG: *v = t.ln_seg; return IXH_OK;
+  case IXH_OPT_FUSE_RES: *v = t.fuse_res; return IXH_OK;
   default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
   }
 }
@@ -775,13 +780,45 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   ln.seg = tune.ln_seg;
   const double ln_bytes = dN * (4 * dH + dH + 4);
 
+  // the residual GEMMs fused with quantizeA of their input and the next
+  // LayerNorm + quantizeA (gemm_res.hip), where the shapes allow it
+  const bool fuse_res = tune.fuse_res != 0 && gemm_res_supported(H, KpH, m->layers[0].o.np) &&
+                        gemm_res_supported(H, KpI, m->layers[0].omlp.np);
+  auto res = [&](const Mat &M, const float *A, int K, const float *gamma) {
+    ResArgs r{};
+    r.A = A;
+    r.lda = K;
+    r.K = K;
+    r.Kp = M.kp;
+    r.Bk = M.qk.as<int8_t>();
+    r.Np = M.np;
+    r.sb = M.sb.as<float>();
+    r.zc = M.zc.as<float>();
+    r.c128 = M.c128.as<int32_t>();
+    r.X = w->x.as<float>();
+    r.M = N;
+    r.H = H;
+    r.gamma = gamma;
+    r.eps = c.norm_eps;
+    r.Q = w->xq.as<int8_t>();
+    r.ldq = KpH;
+    r.SA = w->sa.as<float>();
+    return r;
+  };
+  // bytes of a fused residual GEMM: input rows f32, weights, x read and
+  // written, the quantised LayerNorm output
+  auto res_bytes = [&](double k, bool ln_out) {
+    return dN * 4 * k + k * dH + 12 * dH + dN * 8 * dH + (ln_out ? dN * (dH + 4) : 0);
+  };
+  bool ln_done = false;  // the attn_norm LayerNorm of this layer ran in the previous WoMLP
   for (int l = 0; l < c.layers; l++) {
     const auto &L = m->layers[l];
     const bool global = l % c.global_every == 0;  // Config.IsGlobal
-    if (l > 0) {
+    if (l > 0 && !ln_done) {
       ln.gamma = L.attn_norm.as<float>();
       RUN("ln_quant", 0, ln_bytes, launch_rownorm(ln, st));
     }
+    ln_done = false;
     // QKV projection with RoPE on the queries and keys (infer.go:390-399)
     GemmArgs g = gemm(EPI_ROPE, L.qkv, KpH, w->qkv.as<float>(), 3 * H, 3 * H);
     g.rope_cos = global ? rc_g : rc_l;
@@ -809,22 +846,36 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
     const double pairs = global ? keys_global : keys_local;
     RUN(global ? "attn_global" : "attn_local", 4.0 * D * nh * pairs,
         dN * 3 * dH + 8 * dN * nh + dN * dH * 4, launch_attn_main(aa, st));
-    // x += ctx . Wo^T (infer.go:403)
-    RUN("quant_ctx", 0, dN * (4 * dH + dH + 4),
-        launch_quant_rows(w->ctx.as<float>(), H, N, H, w->xq.as<int8_t>(), KpH, w->sa.as<float>(), st));
-    g = gemm(EPI_ACCUM, L.o, KpH, w->x.as<float>(), H, H);
-    RUN("gemm_wo", 2 * dN * dH * dH, gemm_bytes(dH, dH, dH, true), run_gemm(EPI_ACCUM, g, tune, st));
-    // mlp_norm, Wi + GeGLU, x += g . WoMLP^T (infer.go:404-424)
-    ln.gamma = L.mlp_norm.as<float>();
-    RUN("ln_quant", 0, ln_bytes, launch_rownorm(ln, st));
+    // x += ctx . Wo^T (infer.go:403), then mlp_norm (infer.go:404-407)
+    if (fuse_res) {
+      const ResArgs r = res(L.o, w->ctx.as<float>(), H, L.mlp_norm.as<float>());
+      RUN("gemm_wo_ln", 2 * dN * dH * dH, res_bytes(dH, true), launch_gemm_res(r, c.lanes, st));
+    } else {
+      RUN("quant_ctx", 0, dN * (4 * dH + dH + 4),
+          launch_quant_rows(w->ctx.as<float>(), H, N, H, w->xq.as<int8_t>(), KpH, w->sa.as<float>(), st));
+      g = gemm(EPI_ACCUM, L.o, KpH, w->x.as<float>(), H, H);
+      RUN("gemm_wo", 2 * dN * dH * dH, gemm_bytes(dH, dH, dH, true), run_gemm(EPI_ACCUM, g, tune, st));
+      ln.gamma = L.mlp_norm.as<float>();
+      RUN("ln_quant", 0, ln_bytes, launch_rownorm(ln, st));
+    }
+    // Wi + GeGLU, x += g . WoMLP^T (infer.go:408-424)
     g = gemm(EPI_GEGLU, L.i, KpH, w->g.as<float>(), I, I);
     RUN("gemm_wi", 2 * dN * 2 * dI * dH, gemm_bytes(dH, 2 * dI, dI, false),
         run_gemm(EPI_GEGLU, g, tune, st));
-    RUN("quant_g", 0, dN * (4 * dI + dI + 4),
-        launch_quant_rows(w->g.as<float>(), I, N, I, w->xq.as<int8_t>(), KpI, w->sa.as<float>(), st));
-    g = gemm(EPI_ACCUM_MLP, L.omlp, KpI, w->x.as<float>(), H, H);
-    RUN("gemm_womlp", 2 * dN * dH * dI, gemm_bytes(dI, dH, dH, true),
-        run_gemm(EPI_ACCUM_MLP, g, tune, st));
+    if (fuse_res) {
+      // and the next layer's attn_norm (the last layer's final_norm below
+      // writes float32)
+      const bool next = l + 1 < c.layers;
+      const ResArgs r = res(L.omlp, w->g.as<float>(), I, next ? m->layers[l + 1].attn_norm.as<float>() : nullptr);
+      RUN("gemm_womlp_ln", 2 * dN * dH * dI, res_bytes(dI, next), launch_gemm_res(r, c.lanes, st));
+      ln_done = next;
+    } else {
+      RUN("quant_g", 0, dN * (4 * dI + dI + 4),
+          launch_quant_rows(w->g.as<float>(), I, N, I, w->xq.as<int8_t>(), KpI, w->sa.as<float>(), st));
+      g = gemm(EPI_ACCUM_MLP, L.omlp, KpI, w->x.as<float>(), H, H);
+      RUN("gemm_womlp", 2 * dN * dH * dI, gemm_bytes(dI, dH, dH, true),
+          run_gemm(EPI_ACCUM_MLP, g, tune, st));
+    }
   }
   // final_norm (infer.go:427), then the token states, pooling (infer.go:
   // 265-287) and the heads' logits (heads.go:63-74) on the device

@@ -24,6 +24,7 @@ struct Tuning {
                           // 2: as 0 with the residual GEMMs on gemm_ws
   int gemm_tile = 0;      // gemm_i8 tiles: 0 128x128/2 stages, 1 256x128/3, 2 128x128/3
   int ln_seg = 1;         // LayerNorm lanes 8/16: 1 segment kernel, 0 whole-row LDS kernel
+  int fuse_res = 1;       // residual GEMMs fused with quantizeA of their input and the next LN
 };
 
 // ---- int8 GEMM ----------------------------------------------------------
@@ -80,6 +81,30 @@ bool launch_gemm_as(int epi, const GemmArgs &a, hipStream_t s);
 // The warp-specialised GEMM (gemm_ws.hip): same operands and conditions as
 // gemm_as; MFMA waves and epilogue waves hand blocks over through LDS.
 bool launch_gemm_ws(int epi, const GemmArgs &a, hipStream_t s);
+
+// The residual GEMMs fused with the quantisation of their input and the
+// LayerNorm + quantisation of their output (gemm_res.hip): X[m][:H] +=
+// deq(quantizeA(A[m][:K]) . B^T), then, with gamma, Q/SA = quantizeA(
+// LayerNorm(X[m], gamma)). Needs Np == H and (H, Kp) one of (768, 768),
+// (768, 1152), (256, 256), (256, 512); returns false (nothing launched)
+// otherwise.
+struct ResArgs {
+  const float *A;        // [M][lda] float32 input rows, K valid columns (K % 4 == 0)
+  int lda, K, Kp;
+  const int8_t *Bk;      // weights K-blocked [Kp/32][Np][32]
+  int Np;
+  const float *sb, *zc;  // [Np]
+  const int32_t *c128;   // [Np]
+  float *X;              // [M][H] residual, updated in place
+  int M, H;
+  const float *gamma;    // [H] LayerNorm weight of the new x, or nullptr (no LayerNorm)
+  double eps;
+  int8_t *Q;             // [M][ldq] quantised LayerNorm output
+  int ldq;
+  float *SA;             // [M] its scales
+};
+bool gemm_res_supported(int H, int Kp, int Np);
+bool launch_gemm_res(const ResArgs &a, int lanes, hipStream_t s);
 
 // ---- host helpers (ixh_api.cpp) ---------------------------------------------
 // Sets the calling thread's ixh_last_error message; returns code.

@@ -257,3 +257,26 @@ def test_qkv_heads_per_workgroup(nheads):
     want, _ = ora.encode_tokens(seqs)
     assert f32_bits_equal(got, want), mismatch_report(got, want)
     assert f32_bits_equal(pooled, ora.encode_seqs(seqs))
+
+
+@pytest.mark.parametrize("shape,lanes", [("small", 0), ("small", 4), ("small", 8), ("small", 16),
+                                         ("base", 8), ("base", 16), ("base", 0)])
+def test_fused_residual_gemms(shape, lanes):
+    """Option fuse_res (default on): Wo and WoMLP fused with quantizeA of
+    their input rows and the next LayerNorm + quantizeA (gemm_res.hip) give
+    the separate kernels' bits and the oracle's, for every lane width of
+    the LayerNorm chains, at both model widths, with row counts that leave
+    a partial 32-row block and a last layer without LayerNorm."""
+    cfg = small_cfg(layers=3) if shape == "small" else base_cfg(layers=2)
+    w, gpu, ora = model_pair(cfg, seed=71, lanes=lanes)
+    rng = np.random.default_rng(71 + lanes)
+    seqs = ids_uniform_lengths(rng, 7, 1, 300, cfg.vocab)
+    if sum(len(s) for s in seqs) % 32 == 0:
+        seqs.append(rng.integers(0, cfg.vocab, size=5, dtype=np.int32))
+    with options(gpu, fuse_res=1):
+        fused = gpu.encode_tokens(seqs)
+    with options(gpu, fuse_res=0):
+        separate = gpu.encode_tokens(seqs)
+    assert f32_bits_equal(fused, separate), mismatch_report(fused, separate)
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(fused, want), mismatch_report(fused, want)
