@@ -132,6 +132,79 @@ def serving(np, model, cfg, args):
     }), flush=True)
 
 
+def decide(np, model, cfg, args):
+    """DecideInputs-shaped load (model.go:316-330, spans.go:369-383): many
+    short inputs, each through the encoder and three pooled-row heads
+    (Choice-8, Noul, a 5-option Score: 8 + 1 + 4 logits). Three ways:
+      reference: sorted by length, sequential passes of 32 sequences
+        (forEachPooled's batchSize, model.go:391-417), pooled rows to the
+        host, head.logits there in float64 (heads.go:63-74);
+      heads_32: the same passes with the heads on the device
+        (ixh_encode_heads), only the logits leaving the GPU;
+      heads_all: every input in one ixh_encode_heads call (the library cuts
+        passes of at most pass_tokens tokens).
+    Host ids in, host logits out; the logits of the three are checked equal
+    (the device and host sums are in the same order)."""
+    from indecis_amd import heads as hd
+    rng = np.random.default_rng(7)
+    n = args.inputs
+    lens = rng.integers(args.decide_lo, args.decide_hi + 1, size=n)
+    seqs = [rng.integers(0, cfg.vocab, size=int(k), dtype=np.int32) for k in lens]
+    heads = []
+    for rows in (8, 1, 4):
+        w, b = hd.random_head(rows, cfg.hidden, rng)
+        heads.append((w, rng.standard_normal(rows).astype(np.float32), False))
+    model.set_heads(heads)
+    W = np.concatenate([h[0] for h in heads]).astype(np.float64)
+    bias = np.concatenate([h[1] for h in heads]).astype(np.float64)
+    order = sorted(range(n), key=lambda i: len(seqs[i]))
+    ntok = int(lens.sum())
+
+    def reference():
+        z = np.zeros((n, W.shape[0]))
+        for s0 in range(0, n, 32):
+            idx = order[s0:s0 + 32]
+            pooled = model.encode_seqs([seqs[i] for i in idx]).astype(np.float64)
+            z[idx] = pooled @ W.T + bias
+        return z
+
+    def heads_32():
+        z = np.zeros((n, W.shape[0]))
+        for s0 in range(0, n, 32):
+            idx = order[s0:s0 + 32]
+            zp, _ = model.encode_heads([seqs[i] for i in idx], tokens=False)
+            z[idx] = zp
+        return z
+
+    def heads_all():
+        zp, _ = model.encode_heads([seqs[i] for i in order], tokens=False)
+        z = np.zeros((n, W.shape[0]))
+        z[order] = zp
+        return z
+
+    res = {}
+    outs = {}
+    for name, fn in (("reference", reference), ("heads_32", heads_32), ("heads_all", heads_all)):
+        fn()  # warm-up: workspaces of these shapes
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            outs[name] = fn()
+        dt = (time.perf_counter() - t0) / args.steps
+        res[name] = {"inputs_per_s": round(n / dt, 1), "tokens_per_s": round(ntok / dt, 1),
+                     "ms_per_call": round(dt * 1e3, 3)}
+    same = (np.array_equal(outs["heads_32"], outs["heads_all"]) and
+            np.allclose(outs["reference"], outs["heads_all"], rtol=1e-9, atol=1e-12))
+    print(json.dumps({
+        "metric": "decision-path inputs/s (DecideInputs: encoder + pooled-row heads)",
+        "value": res["heads_all"]["inputs_per_s"], "unit": "inputs/s", "higher_is_better": True,
+        "n_gpus": 1, "steps": args.steps, "data": "synthetic",
+        "config": {"workload": f"{n} inputs of U[{args.decide_lo},{args.decide_hi}] tokens, base shape, "
+                               "Choice-8 + Noul + Score-5 heads", "tokens": ntok},
+        "modes": res, "logits_agree": bool(same),
+        "speedup_vs_reference_shape": round(res["heads_all"]["inputs_per_s"] / res["reference"]["inputs_per_s"], 2),
+    }), flush=True)
+
+
 def tokenize(np, args):
     """Host tokenizer throughput (tokenizer.go's EncodeMax on many texts):
     ixh_tokenizer_encode_batch on the box's CPU share, beside Hugging Face
@@ -244,6 +317,11 @@ def main():
     ap.add_argument("--tokenize", action="store_true",
                     help="instead: host tokenizer throughput, and text to pooled rows for one batch")
     ap.add_argument("--docs", type=int, default=4096, help="documents (--tokenize)")
+    ap.add_argument("--decide", action="store_true",
+                    help="instead: a DecideInputs-shaped load, 32-sequence passes vs heads on the device")
+    ap.add_argument("--inputs", type=int, default=8192, help="inputs (--decide)")
+    ap.add_argument("--decide-lo", type=int, default=8)
+    ap.add_argument("--decide-hi", type=int, default=256)
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -272,6 +350,10 @@ def main():
     model = Model(weights, device=0, lanes=args.lanes)
     if args.serving:
         serving(np, model, cfg, args)
+        model.close()
+        return
+    if args.decide:
+        decide(np, model, cfg, args)
         model.close()
         return
     ids_d = torch.from_numpy(np.concatenate(seqs)).to("cuda")
