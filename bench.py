@@ -51,25 +51,72 @@ def make_inputs(np, vocab, B, lo, hi, seed=20261201):
     return seqs
 
 
+def _host_info():
+    """The host CPU model and the Go toolchain, if any (the reference itself
+    needs Go 1.27 with GOEXPERIMENT=simd)."""
+    import shutil
+    import subprocess
+    cpu = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    go = shutil.which("go")
+    ver = None
+    if go:
+        try:
+            ver = subprocess.run([go, "version"], capture_output=True, text=True, timeout=20).stdout.strip()
+        except (OSError, subprocess.SubprocessError):
+            ver = "go present, version unreadable"
+    return {"cpu": cpu, "go": ver}
+
+
 def cpu_baseline(np, weights, seqs, max_tokens):
-    """Times the oracle (C restatement of the reference int8 path, OpenMP)
-    on the first sequences of the batch, up to max_tokens tokens."""
+    """Times the CPU restatement of the reference's int8 path (oracle/:
+    OpenMP, MatMul8N and Attn8's products on VPDPBUSD tiles as the
+    reference's VNNI kernels compute them, bit-identical to the checker)
+    on the first sequences of the batch up to max_tokens tokens, on every
+    host thread, then on one thread over a sixth of that sample."""
     from oracle import oracle as orc
-    sample, n = [], 0
-    for s in seqs:
-        if n + len(s) > max_tokens and sample:
-            break
-        sample.append(s)
-        n += len(s)
+
+    def sample_of(limit):
+        sample, n = [], 0
+        for s in seqs:
+            if n + len(s) > limit and sample:
+                break
+            sample.append(s)
+            n += len(s)
+        return sample, n
+
     om = orc.OracleModel(weights, lanes=8)
-    om.encode_seqs(sample[:1])  # warm-up
-    t0 = time.perf_counter()
-    om.encode_seqs(sample)
-    dt = time.perf_counter() - t0
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    level = orc.set_gemm(1)
+    L = orc.lib()
+    cores = L.ixo_max_threads()
+    res = {}
+    try:
+        for threads, limit in ((cores, max_tokens), (1, max(512, max_tokens // 6))):
+            L.ixo_set_threads(threads)
+            sample, n = sample_of(limit)
+            om.encode_seqs(sample[:1])  # warm-up
+            t0 = time.perf_counter()
+            om.encode_seqs(sample)
+            dt = time.perf_counter() - t0
+            res[threads] = (n, len(sample), dt)
+    finally:
+        L.ixo_set_threads(cores)
+        orc.set_gemm(0)
+    n, b, dt = res[cores]
+    n1, b1, dt1 = res[1]
+    kind = {2: "AVX-512 VNNI", 1: "AVX-VNNI", 0: "no VNNI: plain loops"}[level]
     return {"value": round(n / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"first {len(sample)} sequences ({n} tokens) of the same batch, "
-                      f"{dt:.1f} s, C restatement of linalg/modernbert int8 (OpenMP), not the Go reference"}
+            "sample": f"first {b} sequences ({n} tokens) of the same batch, {dt:.1f} s; C restatement of "
+                      f"linalg/modernbert int8 with {kind} 6x16 tiles (OpenMP), not the Go reference",
+            "single_core": {"value": round(n1 / dt1, 2), "unit": "tokens/s",
+                            "sample": f"first {b1} sequences ({n1} tokens), {dt1:.1f} s"},
+            "host": _host_info()}
 
 
 def load_traffic(kernel, workload):
@@ -304,7 +351,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="cfg4", choices=sorted(WORKLOADS))
     ap.add_argument("--lanes", type=int, default=8)
-    ap.add_argument("--cpu-tokens", type=int, default=24576,
+    ap.add_argument("--cpu-tokens", type=int, default=32768,
                     help="tokens of the batch timed on the CPU baseline (0: skip)")
     ap.add_argument("--parts", type=int, default=0,
                     help="run every phase with the batch in this many parts (profiling runs: 1)")

@@ -2,7 +2,8 @@
 
 The reference (Go 1.27 + GOEXPERIMENT=simd + Go assembly) cannot be built
 in this image: there is no Go toolchain, so there is no oracle/_ref build.
-The oracle is the C restatement in indecis_oracle.c.
+The oracle is the C restatement in indecis_oracle.c; vnni.c adds the
+VPDPBUSD-tiled GEMM the timed CPU baseline uses (same bits).
 """
 import os
 import subprocess
@@ -17,9 +18,9 @@ CFLAGS = ["-O3", "-march=x86-64-v3", "-ffp-contract=off", "-fno-fast-math",
 
 
 def build(verbose=False):
-    src = os.path.join(HERE, "indecis_oracle.c")
+    srcs = [os.path.join(HERE, f) for f in ("indecis_oracle.c", "vnni.c")]
     tmp = SO + ".tmp"
-    cmd = ["gcc", *CFLAGS, src, "-o", tmp, "-lm"]
+    cmd = ["gcc", *CFLAGS, *srcs, "-o", tmp, "-lm"]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

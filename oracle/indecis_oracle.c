@@ -149,6 +149,7 @@ void ixo_b8_to_panels(const int8_t *q, int k, int n, int8_t *panels) {
  * q = 0 (the reference fills 128, i.e. 0 after the offset). */
 void ixo_quantize_rows(const float *a, int lda, int m, int k, int8_t *q,
                        int ldq, float *sa) {
+#pragma omp parallel for schedule(static)
   for (int i = 0; i < m; i++) {
     const float *x = a + (size_t)i * lda;
     int8_t *row = q + (size_t)i * ldq;
@@ -194,6 +195,9 @@ void ixo_matmul8_deq(float *c, int ldc, const int8_t *q, int ldq,
                      const float *sa, const int8_t *w, const float *sb,
                      const int32_t *colsum, int m, int k, int n,
                      int accumulate) {
+  /* the timed CPU baseline's VNNI tiles (vnni.c), when selected */
+  if (ixo_gemm_kind() && ixo_matmul8_deq_vnni(c, ldc, q, ldq, sa, w, sb, colsum, m, k, n, accumulate))
+    return;
 #pragma omp parallel for schedule(static)
   for (int i = 0; i < m; i++) {
     const int8_t *a = q + (size_t)i * ldq;
@@ -468,6 +472,8 @@ void ixo_attend8(float *o, int ldo, const float *q, const float *k,
                  const float *v, int ld, int n, int D, int window,
                  float scale, int lanes) {
   if (n <= 0) return;
+  /* the timed CPU baseline's VNNI products (vnni.c), when selected */
+  if (ixo_gemm_kind() && ixo_attend8_vnni(o, ldo, q, k, v, ld, n, D, window, scale, lanes)) return;
   int8_t *qq = (int8_t *)malloc((size_t)n * D);
   int8_t *kq = (int8_t *)malloc((size_t)n * D);
   int8_t *vq = (int8_t *)malloc((size_t)n * D);

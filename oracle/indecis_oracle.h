@@ -109,6 +109,21 @@ void ixo_attend8(float *o, int ldo, const float *q, const float *k,
                  const float *v, int ld, int n, int D, int window,
                  float scale, int lanes);
 
+/* The CPU baseline's GEMM (vnni.c): ixo_set_gemm(1) makes MatMul8N use
+ * 6x16 VPDPBUSD tiles (AVX-512 VNNI or AVX-VNNI, chosen at run time; the
+ * same bits); 0 (default) the plain restatement. ixo_vnni_level: 2
+ * AVX-512 VNNI, 1 AVX-VNNI, 0 none; ixo_gemm_kind: the level in use. */
+void ixo_set_gemm(int kind);
+int ixo_vnni_level(void);
+int ixo_gemm_kind(void);
+int ixo_matmul8_deq_vnni(float *c, int ldc, const int8_t *q, int ldq, const float *sa,
+                         const int8_t *w, const float *sb, const int32_t *colsum, int m, int k,
+                         int n, int accumulate);
+void ixo_set_threads(int n);
+int ixo_max_threads(void);
+int ixo_attend8_vnni(float *o, int ldo, const float *q, const float *k, const float *v, int ld, int n,
+                     int D, int window, float scale, int lanes);
+
 /* Attn8.Attend blocked as the reference blocks it (48 queries, 16-key
  * panels), queries [i0, i1) into o[(i - i0)*ldo]; plant 1 or 2 plants a
  * mistake (exclusive window bound; 1/(255 sum e) normalisation). */

@@ -90,6 +90,13 @@ def lib():
         L.ixo_encode.restype = C.c_int
         L.ixo_pool.argtypes = [f32p, i32p, C.c_int, C.c_int, C.c_int, f32p]
         L.ixo_embed_row.argtypes = [C.POINTER(IxoModel), C.c_int32, f32p]
+        L.ixo_set_gemm.argtypes = [C.c_int]
+        L.ixo_set_gemm.restype = None
+        L.ixo_vnni_level.restype = C.c_int
+        L.ixo_gemm_kind.restype = C.c_int
+        L.ixo_set_threads.argtypes = [C.c_int]
+        L.ixo_set_threads.restype = None
+        L.ixo_max_threads.restype = C.c_int
         L.ixo_head_logits.argtypes = [f32p, C.c_int, C.c_int, f32p, f32p, C.c_int, f64p]
         _lib = L
     return _lib
@@ -264,6 +271,14 @@ def attend8(q, k, v, window=-1, scale=0.125, lanes=8):
     if n:
         lib().ixo_attend8(o, D, q, k, v, D, n, D, window, scale, lanes)
     return o
+
+
+def set_gemm(kind):
+    """MatMul8N of the oracle: 0 the plain restatement (the checker), 1 the
+    VPDPBUSD tiles of vnni.c where the CPU has VNNI (the timed baseline).
+    Returns the VNNI level in use (2 AVX-512, 1 AVX-VNNI, 0 plain)."""
+    lib().ixo_set_gemm(int(kind))
+    return lib().ixo_gemm_kind()
 
 
 def attend8_blocked(o, off, ldo, q, k, v, i0, i1, window=-1, scale=0.125, lanes=8, plant=0):

@@ -723,3 +723,48 @@ def test_encoder_rejects_bad_ids(small_model):
     w, om = small_model
     with pytest.raises(ValueError, match="out of vocabulary"):
         om.encode_tokens([np.array([1, w.cfg.vocab], np.int32)])
+
+
+def test_vnni_gemm_equals_restatement():
+    """The timed CPU baseline's MatMul8N (vnni.c: 6x16 VPDPBUSD tiles on
+    the PackedB8 panels, kernel_vnni_amd64.s) gives the plain
+    restatement's bits, stored and accumulated, on ragged shapes (rows not
+    a multiple of 6, depth not of 4, columns not of 16); so do Attn8's
+    products on VPDPBUSD (every window kind and lane width); and the
+    encoder built on them gives the oracle encoder's bits."""
+    if orc.lib().ixo_vnni_level() == 0:
+        pytest.skip("no VNNI on this CPU")
+    rng = np.random.default_rng(81)
+    try:
+        for m, k, n in [(1, 4, 1), (7, 70, 40), (13, 257, 19), (64, 768, 2304), (33, 1152, 768)]:
+            a = (rng.standard_normal((m, k)) * 2).astype(np.float32)
+            q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+            s = rng.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+            cs = q.astype(np.int32).sum(axis=1).astype(np.int32)
+            c0 = rng.standard_normal((m, n)).astype(np.float32)
+            for acc in (False, True):
+                orc.set_gemm(0)
+                want = orc.matmul8(a, q, s, cs, c=c0, accumulate=acc)
+                assert orc.set_gemm(1) > 0
+                got = orc.matmul8(a, q, s, cs, c=c0, accumulate=acc)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, k, n, acc)
+        # Attn8's products (scores 16 keys a panel, P.V 16 dimensions a panel)
+        for n in (1, 5, 17, 290):
+            q, k, v = (rng.standard_normal((n, 64)).astype(np.float32) for _ in range(3))
+            for window in (-1, 3, 64):
+                for lanes in (0, 8, 16):
+                    orc.set_gemm(0)
+                    want = orc.attend8(q, k, v, window, 0.125, lanes)
+                    orc.set_gemm(1)
+                    got = orc.attend8(q, k, v, window, 0.125, lanes)
+                    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, window, lanes)
+        cfg = small_cfg(layers=2)
+        w = Weights.random(cfg, seed=81)
+        seqs = ids_uniform_lengths(rng, 5, 1, 120, cfg.vocab)
+        orc.set_gemm(0)
+        want, _ = orc.OracleModel(w, lanes=8).encode_tokens(seqs)
+        orc.set_gemm(1)
+        got, _ = orc.OracleModel(w, lanes=8).encode_tokens(seqs)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    finally:
+        orc.set_gemm(0)
