@@ -197,7 +197,9 @@ enum {
   IXH_OPT_GEMM_TILE = 5,   /* tiled GEMM: 0 (default) 128x128 2 stages, 1 256x128 3, 2 128x128 3 */
   IXH_OPT_LN_SEG = 6,      /* LayerNorm at lanes 8/16: 1 (default) segment kernel, 0 whole-row */
   IXH_OPT_FUSE_RES = 7,    /* 1 (default): Wo and WoMLP fused with the quantisation of their
-                              input and the next LayerNorm + quantisation; 0: separate kernels */
+                              input and the next LayerNorm + quantisation; 2: Wo's input
+                              streamed in its K loop (attention writes row maxima); 3: also
+                              WoMLP's (the GeGLU epilogue writes them); 0: separate kernels */
 };
 int ixh_model_set_option(ixh_model *m, int option, int64_t value);
 int ixh_model_get_option(ixh_model *m, int option, int64_t *value);

@@ -577,6 +577,7 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   const float sp = 1.0f / (float)(int)psum;
   const float *vsd = a.vs + ((size_t)b * a.nh + h) * D;
   float *orow = a.ctx + (size_t)(base + qi) * H + h * D;
+  float mx = 0.f;  // max |ctx| of this (row, head), for the fused Wo GEMM
 #pragma unroll
   for (int dt = 0; dt < 2; dt++) {
 #pragma unroll
@@ -590,9 +591,14 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
         const int r = 4 * g + u;
         const int tile = o[dt][r];
         ov[u] = (((float)tile - 0.0f) * vv[u]) * sp;
+        mx = __builtin_fmaxf(mx, fabsf(ov[u]));
       }
       *(float4 *)(orow + d0) = make_float4(ov[0], ov[1], ov[2], ov[3]);
     }
+  }
+  if (a.rmax) {
+    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));  // the other 32 dimensions
+    if (lane < 32) a.rmax[(size_t)(base + qi) * a.nh + h] = mx;
   }
 }
 

@@ -90,7 +90,9 @@ __global__ __launch_bounds__(256, 2) void gemm_as_kernel(GemmArgs a, int units, 
   v16i acc[MB][2], pacc[MB][2];
   // the pending block (wave-uniform state). Before the first block there is
   // none: its slices run on a descriptor of size 0, so they store nothing.
-  int p_m0 = 0, p_n = 0, p_par = 0;
+  // (p_m0 starts past the last row: the phantom block's row maxima are not
+  // written either)
+  int p_m0 = a.M, p_n = 0, p_par = 0;
   int c1[2];
   float zc[2], sb[2];
   // stores (and EPI_ACCUM's residual loads): C, or Ci for EPI_TILE
@@ -127,7 +129,15 @@ __global__ __launch_bounds__(256, 2) void gemm_as_kernel(GemmArgs a, int units, 
         // vec_simd.go:125-160, FMA form on the multiple-of-16 prefix)
         const int gc = p_n / 2 + fr;
         const float ge = gc < a.n_gelu ? gelu_fma(v0) : gelu_scalar(v0);
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(ge * v1), crs, pvo[0], so, 0);
+        const float gv = ge * v1;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(gv), crs, pvo[0], so, 0);
+        if (a.rmax) {
+          // max |g| of the row over these 32 gated columns, for the fused
+          // residual GEMM that quantises g (quantizeA's max, in parts)
+          const float mx = halfwave_max(fabsf(gv));
+          const int row = p_m0 + rw + 4 * fh, part = p_n / 64;
+          if (fr == 16 && row < a.M && part < a.rmax_ld) a.rmax[(size_t)row * a.rmax_ld + part] = mx;
+        }
       } else if constexpr (EPI == EPI_ACCUM || EPI == EPI_ACCUM_MLP) {
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(old[rs][0] + v0), crs, pvo[0], so, 0);
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(old[rs][1] + v1), crs, pvo[1], so, 0);

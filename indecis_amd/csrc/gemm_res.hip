@@ -34,6 +34,15 @@
 //     across the waves, q8(o, 1/s) staged as bytes, stored as 16-byte rows.
 // Without gamma (the last layer, whose final_norm writes float32) steps 4
 // and 5 are skipped.
+//
+// Streamed input (STREAM, when the kernel that wrote A also wrote maxima
+// of |A| over parts of each row: attention per head, the GeGLU epilogue
+// per 32 columns): step 1 only reads those maxima — quantizeA's max|a| is
+// their max, exactly — and the K loop brings A in K step by K step
+// (32 rows x 32 columns of float32, a float4 a thread, PA steps ahead),
+// quantises it and writes it to a 3-stage LDS ring read by the MFMAs, one
+// barrier a step. The input rows then stream from HBM while the MFMAs run
+// instead of in a bulk load before them.
 #include <algorithm>
 
 #include "ixh_device.h"
@@ -45,17 +54,28 @@ namespace gemm_res_impl {
 
 constexpr int BM = 32;  // rows of a workgroup
 constexpr int PF = 2;   // K steps of weight fragments in flight
+constexpr int PA = 12;  // K steps of streamed input in flight (STREAM)
 
-template <int KT, int NB, int V, bool LN>
+// Workgroup barrier for the LDS ring: this wave's LDS accesses complete
+// (lgkmcnt 0), then s_barrier; the wave's global loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt 63, expcnt 7, lgkmcnt 0
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int KT, int NB, int V, bool LN, bool STREAM>
 __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   constexpr int Kp = 32 * KT;
   constexpr int QC = 32 * NB;     // columns of a wave
   constexpr int H = 4 * QC;
   constexpr int XLD = QC + 8;     // floats per staged row (conflict-free chains)
   constexpr int CPL = (Kp + 255) / 256;  // float4 a lane per input row
+  constexpr int PANEL = STREAM ? 3 * BM * 32 : BM * Kp;  // ring of 3 K steps, or the whole panel
   extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
-  int8_t *const panel = smem;                        // [BM][Kp]
-  float *const xs = (float *)(smem + BM * Kp);       // [BM][XLD], then [BM][H] bytes
+  int8_t *const panel = smem;                        // [BM][Kp] or 3 x [BM][32]
+  float *const xs = (float *)(smem + PANEL);         // [BM][XLD], then [BM][H] bytes
   __shared__ float sa_s[BM];
   __shared__ float red_s[4][BM];
   __shared__ float mean_s[BM], rstd_s[BM];
@@ -80,6 +100,36 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
 #pragma unroll
   for (int s = 0; s < PF; s++) loadB(s, bq[s]);
 
+  // streamed input: thread t loads columns 32kt + 4(t%8) .. +3 of row t/8
+  const int ar = tid >> 3, ac = 4 * (tid & 7);
+  const float *asrc = a.A + (size_t)min(m0 + ar, M - 1) * a.lda + ac;  // rows past M: never stored
+  float4 av[STREAM ? PA : 1];
+  if constexpr (STREAM) {
+#pragma unroll
+    for (int s = 0; s < PA; s++)
+      if (s < KT) av[s] = *(const float4 *)(asrc + 32 * s);
+  }
+
+  float inv_r = 0.f;  // STREAM: 1/s of row ar
+  if constexpr (STREAM) {
+    // ---- 1. the row scales from the maxima of the row's parts ----
+    if (tid < BM) {
+      float mx = 0.f;
+      if (m0 + tid < M) {
+        const float *am = a.amax + (size_t)(m0 + tid) * a.P;
+        for (int p = 0; p < a.P; p++) mx = fmax32(mx, am[p]);
+      }
+      float s = 0.f, inv = 0.f;
+      if (mx != 0.f) {  // quantizeA: s = max/127, inv = 1/s (int8.go:175-183)
+        s = mx / 127.0f;
+        inv = 1.0f / s;
+      }
+      sa_s[tid] = s;
+      red_s[0][tid] = inv;
+    }
+    __syncthreads();
+    inv_r = red_s[0][ar];
+  } else {
   // ---- 1. quantizeA of the 32 input rows into the LDS panel ----
   // wave w: rows 8w .. 8w+7, every load in flight at once (RB rows a
   // batch); lane: columns 4(lane + 64c)
@@ -128,6 +178,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
     }
   }
   __syncthreads();
+  }  // !STREAM
 
   // ---- 2. the K loop ----
   v16i acc[NB];
@@ -135,6 +186,30 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   for (int j = 0; j < NB; j++)
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[j][r] = 0;
+  if constexpr (STREAM) {
+    // ring stage s: [32 rows][32 bytes]; thread t writes its 4 bytes, lane
+    // (fr, fh) of a wave reads row fr, bytes 16fh .. 16fh+15
+    auto put = [&](int kt) {
+      const float4 v = av[kt % PA];
+      const int q0 = q8(v.x, inv_r), q1 = q8(v.y, inv_r), q2 = q8(v.z, inv_r), q3 = q8(v.w, inv_r);
+      *(int *)(panel + (kt % 3) * (BM * 32) + ar * 32 + ac) =
+          (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+      if (kt + PA < KT) av[kt % PA] = *(const float4 *)(asrc + 32 * (kt + PA));
+    };
+    put(0);
+    lds_barrier();
+#pragma unroll
+    for (int kt = 0; kt < KT; kt++) {
+      // stage kt+1 is free: its last readers (step kt-2) passed the
+      // barrier of step kt-1
+      if (kt + 1 < KT) put(kt + 1);
+      const v4i fa = *(const v4i *)(panel + (kt % 3) * (BM * 32) + fr * 32 + 16 * fh);
+#pragma unroll
+      for (int j = 0; j < NB; j++) acc[j] = mfma32(fa, bq[kt % PF][j], acc[j]);
+      if (kt + PF < KT) loadB(kt + PF, bq[kt % PF]);
+      lds_barrier();  // stage kt+1 written by every thread
+    }
+  } else {
   const int8_t *pa = panel + fr * Kp;
   auto loadA = [&](int kt) -> v4i {
     const int c = 2 * kt + fh;
@@ -150,6 +225,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
     if (kt + PF < KT) loadB(kt + PF, bq[kt % PF]);
     fa = fn;
   }
+  }  // !STREAM
 
   // ---- 3. the reference tile, dequantised, added to x ----
   // x through a descriptor over the block's rows (rows past M read 0 and
@@ -322,32 +398,34 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   }
 }
 
-template <int KT, int NB, int V, bool LN>
+template <int KT, int NB, int V, bool LN, bool STREAM>
 void launch_one(const ResArgs &a, hipStream_t s) {
-  const size_t shm = (size_t)BM * 32 * KT + (size_t)BM * (32 * NB + 8) * 4;
+  const size_t shm = (size_t)(STREAM ? 3 * BM * 32 : BM * 32 * KT) + (size_t)BM * (32 * NB + 8) * 4;
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void *)gemm_res_kernel<KT, NB, V, LN>,
+    (void)hipFuncSetAttribute((const void *)gemm_res_kernel<KT, NB, V, LN, STREAM>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
     attr = true;
   }
-  gemm_res_kernel<KT, NB, V, LN><<<(a.M + BM - 1) / BM, 256, shm, s>>>(a);
+  gemm_res_kernel<KT, NB, V, LN, STREAM><<<(a.M + BM - 1) / BM, 256, shm, s>>>(a);
 }
 
-template <int KT, int NB, bool LN>
+template <int KT, int NB, bool LN, bool STREAM>
 bool launch_v(const ResArgs &a, int lanes, hipStream_t s) {
   switch (lanes) {
-  case 0: launch_one<KT, NB, 0, LN>(a, s); return true;
-  case 4: launch_one<KT, NB, 4, LN>(a, s); return true;
-  case 8: launch_one<KT, NB, 8, LN>(a, s); return true;
-  case 16: launch_one<KT, NB, 16, LN>(a, s); return true;
+  case 0: launch_one<KT, NB, 0, LN, STREAM>(a, s); return true;
+  case 4: launch_one<KT, NB, 4, LN, STREAM>(a, s); return true;
+  case 8: launch_one<KT, NB, 8, LN, STREAM>(a, s); return true;
+  case 16: launch_one<KT, NB, 16, LN, STREAM>(a, s); return true;
   default: return false;
   }
 }
 
 template <int KT, int NB>
 bool launch_ln(const ResArgs &a, int lanes, hipStream_t s) {
-  return a.gamma ? launch_v<KT, NB, true>(a, lanes, s) : launch_v<KT, NB, false>(a, lanes, s);
+  if (a.amax)
+    return a.gamma ? launch_v<KT, NB, true, true>(a, lanes, s) : launch_v<KT, NB, false, true>(a, lanes, s);
+  return a.gamma ? launch_v<KT, NB, true, false>(a, lanes, s) : launch_v<KT, NB, false, false>(a, lanes, s);
 }
 
 }  // namespace gemm_res_impl
@@ -361,6 +439,7 @@ bool launch_gemm_res(const ResArgs &a, int lanes, hipStream_t s) {
   using namespace gemm_res_impl;
   if (a.M <= 0) return true;
   if (!gemm_res_supported(a.H, a.Kp, a.Np) || a.K > a.Kp || a.K % 4 != 0 || a.ldq < a.H) return false;
+  if (a.amax && (a.K != a.Kp || a.P <= 0 || a.lda % 4 != 0)) return false;
   if (a.H == 768) return a.Kp == 768 ? launch_ln<24, 6>(a, lanes, s) : launch_ln<36, 6>(a, lanes, s);
   return a.Kp == 256 ? launch_ln<8, 2>(a, lanes, s) : launch_ln<16, 2>(a, lanes, s);
 }

@@ -251,6 +251,7 @@ struct Workspace {
   // tabs: the pass's small host-built tables, one copy: offs [B+1], padoff
   // [B+1], blocks [2 nblocks], sequence order [B]
   DevBuf ids, tabs, pos, x, xn, qkv, xq, sa, qq, sq, kp, ks, vt, vs, ctx, g, pooled, flag;
+  DevBuf cmax, gmax;  // row maxima of ctx (per head) and g (per 32 columns)
   DevBuf out_states, out_pooled, out_zp, out_zt;  // host-path staging of a pass's outputs
   PinBuf host, flag_host;
   std::vector<hipEvent_t> events;  // profiling: begin/end pairs, reused
@@ -356,7 +357,7 @@ int set_tuning(Tuning &t, int option, int64_t v, bool model_opts) {
     t.ln_seg = (int)v;
     return IXH_OK;
   case IXH_OPT_FUSE_RES:
-    if (v != 0 && v != 1) return bad();
+    if (v < 0 || v > 3) return bad();
     t.fuse_res = (int)v;
     return IXH_OK;
   default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
@@ -638,7 +639,8 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
       (rc = w->sq.ensure(4 * (size_t)N * nh)) || (rc = w->kp.ensure((size_t)nh * Npad * D)) ||
       (rc = w->ks.ensure(4 * (size_t)nh * Npad)) || (rc = w->vt.ensure((size_t)nh * D * Npad)) ||
       (rc = w->vs.ensure(3 * 4 * (size_t)B * nh * D)) || (rc = w->ctx.ensure(4 * (size_t)N * H)) ||
-      (rc = w->g.ensure(4 * (size_t)N * I)))
+      (rc = w->g.ensure(4 * (size_t)N * I)) || (rc = w->cmax.ensure(4 * (size_t)N * nh)) ||
+      (rc = w->gmax.ensure(4 * (size_t)N * (I / 32))))
     return rc;
 
   // small host-built tables through pinned memory, one copy
@@ -784,11 +786,24 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   // LayerNorm + quantizeA (gemm_res.hip), where the shapes allow it
   const bool fuse_res = tune.fuse_res != 0 && gemm_res_supported(H, KpH, m->layers[0].o.np) &&
                         gemm_res_supported(H, KpI, m->layers[0].omlp.np);
-  auto res = [&](const Mat &M, const float *A, int K, const float *gamma) {
+  // streamed inputs (fuse_res 2: Wo's; 3: Wo's and WoMLP's): attention
+  // writes max |ctx| per (row, head), the GeGLU epilogue on gemm_as max
+  // |g| per (row, 32 columns); fuse_res 1 quantises whole rows into a panel
+  const bool stream_ctx = fuse_res && tune.fuse_res >= 2 && H == KpH;
+  float *const cmax = stream_ctx ? w->cmax.as<float>() : nullptr;
+  aa.rmax = cmax;
+  // the GeGLU maxima exist only where Wi runs on gemm_as (which writes them)
+  float *gmax = nullptr;
+  if (stream_ctx && tune.fuse_res == 3 && I == KpI && tune.gemm != 1 &&
+      gemm_as_supported(gemm(EPI_GEGLU, m->layers[0].i, KpH, nullptr, I, I)))
+    gmax = w->gmax.as<float>();
+  auto res = [&](const Mat &M, const float *A, int K, const float *gamma, const float *amax, int P) {
     ResArgs r{};
     r.A = A;
     r.lda = K;
     r.K = K;
+    r.amax = amax;
+    r.P = P;
     r.Kp = M.kp;
     r.Bk = M.qk.as<int8_t>();
     r.Np = M.np;
@@ -848,7 +863,7 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
         dN * 3 * dH + 8 * dN * nh + dN * dH * 4, launch_attn_main(aa, st));
     // x += ctx . Wo^T (infer.go:403), then mlp_norm (infer.go:404-407)
     if (fuse_res) {
-      const ResArgs r = res(L.o, w->ctx.as<float>(), H, L.mlp_norm.as<float>());
+      const ResArgs r = res(L.o, w->ctx.as<float>(), H, L.mlp_norm.as<float>(), cmax, nh);
       RUN("gemm_wo_ln", 2 * dN * dH * dH, res_bytes(dH, true), launch_gemm_res(r, c.lanes, st));
     } else {
       RUN("quant_ctx", 0, dN * (4 * dH + dH + 4),
@@ -860,13 +875,16 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
     }
     // Wi + GeGLU, x += g . WoMLP^T (infer.go:408-424)
     g = gemm(EPI_GEGLU, L.i, KpH, w->g.as<float>(), I, I);
+    g.rmax = gmax;
+    g.rmax_ld = I / 32;
     RUN("gemm_wi", 2 * dN * 2 * dI * dH, gemm_bytes(dH, 2 * dI, dI, false),
         run_gemm(EPI_GEGLU, g, tune, st));
     if (fuse_res) {
       // and the next layer's attn_norm (the last layer's final_norm below
       // writes float32)
       const bool next = l + 1 < c.layers;
-      const ResArgs r = res(L.omlp, w->g.as<float>(), I, next ? m->layers[l + 1].attn_norm.as<float>() : nullptr);
+      const ResArgs r = res(L.omlp, w->g.as<float>(), I, next ? m->layers[l + 1].attn_norm.as<float>() : nullptr,
+                            gmax, I / 32);
       RUN("gemm_womlp_ln", 2 * dN * dH * dI, res_bytes(dI, next), launch_gemm_res(r, c.lanes, st));
       ln_done = next;
     } else {

@@ -146,6 +146,26 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Max of x over the 32 lanes of each half-wave (lanes 0-31, 32-63) with
+// DPP: rotations inside each 16-lane row, then row 0 (2) into row 1 (3) by
+// row_bcast:15. The result is in lanes 16-31 and 48-63. x must not be NaN.
+__device__ __forceinline__ float halfwave_max(float x) {
+  int v = __float_as_int(x);
+  v = __float_as_int(__builtin_fmaxf(__int_as_float(v),
+                                     __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false))));
+  v = __float_as_int(__builtin_fmaxf(__int_as_float(v),
+                                     __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false))));
+  v = __float_as_int(__builtin_fmaxf(__int_as_float(v),
+                                     __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x122, 0xF, 0xF, false))));
+  v = __float_as_int(__builtin_fmaxf(__int_as_float(v),
+                                     __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x121, 0xF, 0xF, false))));
+  // rows 1 and 3 take the max with lane 15 of the row before; rows 0 and
+  // 2 keep their value (old = v)
+  v = __float_as_int(__builtin_fmaxf(__int_as_float(v),
+                                     __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false))));
+  return __int_as_float(v);
+}
+
 // Dequantisation of one int8 GEMM result (kernel_vnni_amd64.s:144-200):
 // f32(tile) - zc, times sb, times sa — tile being the reference's
 // unsigned-offset integer sum.

@@ -69,6 +69,10 @@ struct GemmArgs {
   float *sq;
   float attn_scale;
   int tile_cfg;  // gemm_i8: 0: 128x128 tiles, 2 LDS stages; 1: 256x128, 3; 2: 128x128, 3
+  // EPI_GEGLU on gemm_as: when not null, rmax[m][c] = max |G[m][32c .. 32c+31]|
+  // for c < rmax_ld (the row maxima the fused residual GEMM quantises by)
+  float *rmax = nullptr;
+  int rmax_ld = 0;
 };
 
 void launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
@@ -91,6 +95,11 @@ bool launch_gemm_ws(int epi, const GemmArgs &a, hipStream_t s);
 struct ResArgs {
   const float *A;        // [M][lda] float32 input rows, K valid columns (K % 4 == 0)
   int lda, K, Kp;
+  // when not null: amax[m][p] (p < P) are maxima of |A[m]| over parts of
+  // the row that together cover it (written by the kernel that wrote A):
+  // the rows are then quantised K step by K step inside the K loop
+  const float *amax;
+  int P;
   const int8_t *Bk;      // weights K-blocked [Kp/32][Np][32]
   int Np;
   const float *sb, *zc;  // [Np]
@@ -188,6 +197,7 @@ struct AttnArgs {
   const int32_t *blocks;   // [nblocks][2]: (sequence, first query)
   int nblocks;
   float *ctx;              // [N][H]
+  float *rmax = nullptr;   // when not null: [N][nh] max |ctx| of each (row, head)
 };
 void launch_attn_quant_q(const AttnArgs &a, hipStream_t s);
 void launch_attn_prologue(const AttnArgs &a, hipStream_t s);

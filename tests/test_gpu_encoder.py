@@ -262,21 +262,24 @@ def test_qkv_heads_per_workgroup(nheads):
 @pytest.mark.parametrize("shape,lanes", [("small", 0), ("small", 4), ("small", 8), ("small", 16),
                                          ("base", 8), ("base", 16), ("base", 0)])
 def test_fused_residual_gemms(shape, lanes):
-    """Option fuse_res (default on): Wo and WoMLP fused with quantizeA of
-    their input rows and the next LayerNorm + quantizeA (gemm_res.hip) give
-    the separate kernels' bits and the oracle's, for every lane width of
-    the LayerNorm chains, at both model widths, with row counts that leave
-    a partial 32-row block and a last layer without LayerNorm."""
+    """Option fuse_res: Wo and WoMLP fused with quantizeA of their input rows
+    and the next LayerNorm + quantizeA (gemm_res.hip), the input quantised
+    into a whole-row panel first (1, the default) or streamed in the K
+    loop from the producers' row maxima (2: Wo's, from attention's maxima
+    per head; 3: also WoMLP's, from the GeGLU epilogue's maxima per 32
+    columns), give the separate kernels' bits (0) and the oracle's, for
+    every lane width of the LayerNorm chains, at both model widths, with
+    row counts that leave a partial 32-row block and a last layer without
+    LayerNorm; also with Wi on gemm_i8 (option gemm 1: no GeGLU maxima,
+    so WoMLP takes the panel while Wo streams)."""
     cfg = small_cfg(layers=3) if shape == "small" else base_cfg(layers=2)
     w, gpu, ora = model_pair(cfg, seed=71, lanes=lanes)
     rng = np.random.default_rng(71 + lanes)
     seqs = ids_uniform_lengths(rng, 7, 1, 300, cfg.vocab)
     if sum(len(s) for s in seqs) % 32 == 0:
         seqs.append(rng.integers(0, cfg.vocab, size=5, dtype=np.int32))
-    with options(gpu, fuse_res=1):
-        fused = gpu.encode_tokens(seqs)
-    with options(gpu, fuse_res=0):
-        separate = gpu.encode_tokens(seqs)
-    assert f32_bits_equal(fused, separate), mismatch_report(fused, separate)
     want, _ = ora.encode_tokens(seqs)
-    assert f32_bits_equal(fused, want), mismatch_report(fused, want)
+    for mode, gemm in ((1, 0), (2, 0), (3, 0), (0, 0), (3, 1)):
+        with options(gpu, fuse_res=mode, gemm=gemm):
+            got = gpu.encode_tokens(seqs)
+        assert f32_bits_equal(got, want), (mode, gemm, mismatch_report(got, want))
