@@ -309,8 +309,22 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
         PUT(t)
         __syncthreads();
         if (wv == 0) {
+          // the sums stay in key order; KB slab reads are issued together
+          // before their KB adds, so the chain waits on LDS once a batch
+          // (KB = 8 where NH = 2 leaves fewer registers)
+          constexpr int KB = NH == 1 ? 16 : 8;
           const int cnt = min(256, n - 256 * t);
-          for (int lr = 0; lr < cnt; lr++) ksum = ksum + slab[lr * KT_LD + lane];
+          const float *col = slab + lane;
+          int lr = 0;
+          for (; lr + KB <= cnt; lr += KB) {
+            float bt[KB];
+#pragma unroll
+            for (int u = 0; u < KB; u++) bt[u] = col[(lr + u) * KT_LD];
+            __builtin_amdgcn_sched_barrier(0);  // every read issued before the first add
+#pragma unroll
+            for (int u = 0; u < KB; u++) ksum = ksum + bt[u];
+          }
+          for (; lr < cnt; lr++) ksum = ksum + col[lr * KT_LD];
         }
         __syncthreads();
       }
