@@ -200,6 +200,9 @@ enum {
                               input and the next LayerNorm + quantisation; 2: Wo's input
                               streamed in its K loop (attention writes row maxima); 3: also
                               WoMLP's (the GeGLU epilogue writes them); 0: separate kernels */
+  IXH_OPT_FUSE_MLP = 8,    /* 1 (default): Wi, GeGLU, the quantisation of g, WoMLP and the next
+                              LayerNorm + quantisation as one kernel (needs FUSE_RES != 0);
+                              0: Wi and WoMLP as chosen by FUSE_RES */
 };
 int ixh_model_set_option(ixh_model *m, int option, int64_t value);
 int ixh_model_get_option(ixh_model *m, int option, int64_t *value);
@@ -377,6 +380,14 @@ int ixh_attend8(int device, float *o, const float *q, const float *k,
  * shortcut from 255*exp(v) of each formula; *undecided: how many v take the
  * fallback. */
 int ixh_check_exp255(int device, int64_t bad[2], float max_err[2], int64_t *undecided);
+
+/* Check of the device GELU (no counterpart in the reference, which computes
+ * GeluMul with IEEE division, linalg/gelu_amd64.s:173-195 and
+ * fastmath.go:9-26): the kernels divide by Markstein's FMA sequence and
+ * clamp with v_med3. For every one of the 2^32 float inputs this counts the
+ * x whose GELU differs in any bit from the IEEE-division form: bad[0] for
+ * the FMA form, bad[1] for the scalar form; both must be 0. */
+int ixh_check_gelu(int device, int64_t bad[2]);
 
 #ifdef __cplusplus
 }

@@ -24,7 +24,7 @@ EXPORTS = [
     "ixh_embed_texts", "ixh_embed_normalize",
     "ixh_matmul8_tile", "ixh_layernorm_quant", "ixh_ln_matmul8_geglu", "ixh_attend8",
     "ixh_model_set_profiling", "ixh_model_set_profile_filter", "ixh_model_profile",
-    "ixh_check_exp255", "ixh_batcher_create", "ixh_batcher_encode", "ixh_batcher_stats",
+    "ixh_check_exp255", "ixh_check_gelu", "ixh_batcher_create", "ixh_batcher_encode", "ixh_batcher_stats",
     "ixh_batcher_destroy", "ixh_model_set_option", "ixh_model_get_option", "ixh_packb8_set_option",
     "ixh_model_set_heads", "ixh_encode_heads", "ixh_matmul8_noalloc",
 ]
@@ -36,10 +36,10 @@ NORM_EMB, NORM_ATTN, NORM_MLP, NORM_FINAL = range(4)
 LAYOUT_ROWS, LAYOUT_PANELS = 0, 1
 OUT_POOLED, OUT_TOKENS = 0, 1
 (OPT_PARTS, OPT_PASS_TOKENS, OPT_QKV_FUSED, OPT_QKV_HEADS, OPT_GEMM, OPT_GEMM_TILE,
- OPT_LN_SEG, OPT_FUSE_RES) = range(8)
+ OPT_LN_SEG, OPT_FUSE_RES, OPT_FUSE_MLP) = range(9)
 OPTIONS = {"parts": OPT_PARTS, "pass_tokens": OPT_PASS_TOKENS, "qkv_fused": OPT_QKV_FUSED,
            "qkv_heads": OPT_QKV_HEADS, "gemm": OPT_GEMM, "gemm_tile": OPT_GEMM_TILE,
-           "ln_seg": OPT_LN_SEG, "fuse_res": OPT_FUSE_RES}
+           "ln_seg": OPT_LN_SEG, "fuse_res": OPT_FUSE_RES, "fuse_mlp": OPT_FUSE_MLP}
 
 
 class IxhError(RuntimeError):
@@ -117,6 +117,7 @@ def lib():
         "ixh_model_profile": [vp, C.POINTER(IxhKernelStat), C.c_int, C.POINTER(C.c_int)],
         "ixh_check_exp255": [C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_float),
                              C.POINTER(C.c_int64)],
+        "ixh_check_gelu": [C.c_int, C.POINTER(C.c_int64)],
         "ixh_batcher_create": [vp, C.c_int, C.c_int, C.POINTER(vp)],
         "ixh_batcher_encode": [vp, vp, vp, C.c_int, vp],
         "ixh_batcher_stats": [vp, C.POINTER(C.c_int64), C.POINTER(C.c_int64)],

@@ -56,15 +56,6 @@ constexpr int BM = 32;  // rows of a workgroup
 constexpr int PF = 2;   // K steps of weight fragments in flight
 constexpr int PA = 12;  // K steps of streamed input in flight (STREAM)
 
-// Workgroup barrier for the LDS ring: this wave's LDS accesses complete
-// (lgkmcnt 0), then s_barrier; the wave's global loads stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt 63, expcnt 7, lgkmcnt 0
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 template <int KT, int NB, int V, bool LN, bool STREAM>
 __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   constexpr int Kp = 32 * KT;
@@ -154,8 +145,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
       for (int c = 0; c < CPL; c++)
         mx = fmax32(mx, fmax32(fmax32(fabsf(v[u][c].x), fabsf(v[u][c].y)),
                                fmax32(fabsf(v[u][c].z), fabsf(v[u][c].w))));
-#pragma unroll
-      for (int t = 1; t < 64; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t));
+      mx = wave_max(mx);
       float s = 0.f, inv = 0.f;
       if (mx != 0.f) {  // quantizeA: s = max/127, inv = 1/s (int8.go:175-183)
         s = mx / 127.0f;
@@ -365,11 +355,12 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
       mx[r] = fmax32(mx[r], fabsf(o));
     }
   }
+  // a half-wave holds one row of each register: its max by DPP (lanes 16-31
+  // and 48-63 get it)
 #pragma unroll
   for (int r = 0; r < 16; r++) {
-#pragma unroll
-    for (int t = 1; t < 32; t <<= 1) mx[r] = fmax32(mx[r], __shfl_xor(mx[r], t));
-    if (fr == 0) red_s[wave][acc_row(r, lane)] = mx[r];
+    mx[r] = halfwave_max(mx[r]);
+    if (fr == 16) red_s[wave][acc_row(r, lane)] = mx[r];
   }
   __syncthreads();
   int8_t *const qs = (int8_t *)xs;  // [BM][H] bytes

@@ -360,6 +360,10 @@ int set_tuning(Tuning &t, int option, int64_t v, bool model_opts) {
     if (v < 0 || v > 3) return bad();
     t.fuse_res = (int)v;
     return IXH_OK;
+  case IXH_OPT_FUSE_MLP:
+    if (v != 0 && v != 1) return bad();
+    t.fuse_mlp = (int)v;
+    return IXH_OK;
   default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
   }
 }
@@ -374,6 +378,7 @@ int get_tuning(const Tuning &t, int option, int64_t *v) {
   case IXH_OPT_GEMM_TILE: *v = t.gemm_tile; return IXH_OK;
   case IXH_OPT_LN_SEG: *v = t.ln_seg; return IXH_OK;
   case IXH_OPT_FUSE_RES: *v = t.fuse_res; return IXH_OK;
+  case IXH_OPT_FUSE_MLP: *v = t.fuse_mlp; return IXH_OK;
   default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
   }
 }
@@ -797,6 +802,11 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   if (stream_ctx && tune.fuse_res == 3 && I == KpI && tune.gemm != 1 &&
       gemm_as_supported(gemm(EPI_GEGLU, m->layers[0].i, KpH, nullptr, I, I)))
     gmax = w->gmax.as<float>();
+  // the whole MLP block as one kernel (mlp_res.hip), where the shapes allow
+  // it; it takes the mlp_norm output quantised by the fused Wo kernel
+  const bool fuse_mlp = fuse_res && tune.fuse_mlp != 0 &&
+                        mlp_res_supported(H, I, KpH, KpI, m->layers[0].i.np) && m->layers[0].i.qk.p &&
+                        m->layers[0].omlp.qk.p && gelu_fma_cols(I, c.lanes) == I;
   auto res = [&](const Mat &M, const float *A, int K, const float *gamma, const float *amax, int P) {
     ResArgs r{};
     r.A = A;
@@ -874,6 +884,37 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
       RUN("ln_quant", 0, ln_bytes, launch_rownorm(ln, st));
     }
     // Wi + GeGLU, x += g . WoMLP^T (infer.go:408-424)
+    if (fuse_mlp) {
+      // and the next layer's attn_norm, in one kernel
+      const bool next = l + 1 < c.layers;
+      MlpArgs ma{};
+      ma.Aq = w->xq.as<int8_t>();
+      ma.sa = w->sa.as<float>();
+      ma.Bi = L.i.qk.as<int8_t>();
+      ma.Npi = L.i.np;
+      ma.sbi = L.i.sb.as<float>();
+      ma.zci = L.i.zc.as<float>();
+      ma.c128i = L.i.c128.as<int32_t>();
+      ma.n_gelu = gelu_fma_cols(I, c.lanes);
+      ma.Bo = L.omlp.qk.as<int8_t>();
+      ma.sbo = L.omlp.sb.as<float>();
+      ma.zco = L.omlp.zc.as<float>();
+      ma.c128o = L.omlp.c128.as<int32_t>();
+      ma.X = w->x.as<float>();
+      ma.M = N;
+      ma.H = H;
+      ma.I = I;
+      ma.gamma = next ? m->layers[l + 1].attn_norm.as<float>() : nullptr;
+      ma.eps = c.norm_eps;
+      ma.Q = w->xq.as<int8_t>();
+      ma.ldq = KpH;
+      ma.SA = w->sa.as<float>();
+      RUN("mlp_ln", 2 * dN * 2 * dI * dH + 2 * dN * dH * dI,
+          dN * (dH + 4) + 3 * dI * dH + 12 * (2 * dI + dH) + dN * 8 * dH + (next ? dN * (dH + 4) : 0),
+          launch_mlp_res(ma, c.lanes, st));
+      ln_done = next;
+      continue;
+    }
     g = gemm(EPI_GEGLU, L.i, KpH, w->g.as<float>(), I, I);
     g.rmax = gmax;
     g.rmax_ld = I / 32;
@@ -2093,6 +2134,25 @@ int ixh_check_exp255(int device, int64_t bad[2], float max_err[2], int64_t *unde
   memcpy(&max_err[0], &e0, 4);
   memcpy(&max_err[1], &e1, 4);
   *undecided = (int64_t)r[4];
+  return IXH_OK;
+}
+
+int ixh_check_gelu(int device, int64_t bad[2]) {
+  if (!bad) return fail(IXH_EINVAL, "linalg: hip: nil result");
+  DEVGUARD(device);
+  TmpStream ts;
+  HIPCK(hipStreamCreateWithFlags(&ts.s, hipStreamNonBlocking));
+  DevBuf dres;
+  int rc;
+  if ((rc = dres.ensure(2 * sizeof(unsigned long long)))) return rc;
+  HIPCK(hipMemsetAsync(dres.p, 0, 2 * sizeof(unsigned long long), ts.s));
+  launch_check_gelu(dres.as<unsigned long long>(), ts.s);
+  LAUNCHCK("check_gelu");
+  unsigned long long r[2];
+  HIPCK(hipMemcpyAsync(r, dres.p, sizeof r, hipMemcpyDeviceToHost, ts.s));
+  HIPCK(hipStreamSynchronize(ts.s));
+  bad[0] = (int64_t)r[0];
+  bad[1] = (int64_t)r[1];
   return IXH_OK;
 }
 

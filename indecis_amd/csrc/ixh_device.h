@@ -93,10 +93,34 @@ __device__ __forceinline__ float exp255_fast(float v) {
   return __builtin_amdgcn_exp2f(__builtin_fmaf(v, 1.44269504088896341f, 7.99435343685885793f));
 }
 
-// GELU (erf) of geluMulAVX2 (linalg/gelu_amd64.s:173-195).
+// p / q for the GELU's rational erf, round to nearest: Markstein's
+// FMA-based division (the reciprocal refined by one Newton step, the
+// quotient corrected by two exact remainders). Here q, the denominator
+// polynomial on t*t in [0, 16], lies in [-2.4, -0.0142] and |p| <= |q|, so
+// no operand needs the range scaling of the general IEEE sequence;
+// ixh_check_gelu verifies, for every float input of both GELU forms, that
+// the GELU result equals the one with IEEE division.
+__device__ __forceinline__ float gelu_div(float p, float q) {
+  float r = __builtin_amdgcn_rcpf(q);
+  r = __builtin_fmaf(__builtin_fmaf(-q, r, 1.0f), r, r);
+  float y = p * r;
+  y = __builtin_fmaf(__builtin_fmaf(-q, y, p), r, y);
+  y = __builtin_fmaf(__builtin_fmaf(-q, y, p), r, y);
+  return y;
+}
+
+// clamp of the GELU argument to [-4, 4] (VMAXPS/VMINPS in the reference):
+// v_med3 gives the same value for every non-NaN t, and a NaN t comes only
+// from a NaN x, whose GELU is NaN through 0.5*x either way.
+__device__ __forceinline__ float gelu_clamp(float t) { return __builtin_amdgcn_fmed3f(t, -4.0f, 4.0f); }
+
+// GELU (erf) of geluMulAVX2 (linalg/gelu_amd64.s:173-195). FAST: gelu_div
+// and gelu_clamp; false: IEEE division and the compare-select clamp (the
+// form ixh_check_gelu compares against).
+template <bool FAST = true>
 __device__ __forceinline__ float gelu_fma(float x) {
   float t = x * 0.7071067811865476f;
-  t = fmin32(fmax32(t, -4.0f), 4.0f);
+  t = FAST ? gelu_clamp(t) : fmin32(fmax32(t, -4.0f), 4.0f);
   float t2 = t * t;
   float p = __builtin_fmaf(t2, -2.72614225801306e-10f, 2.77068142495902e-08f);
   p = __builtin_fmaf(t2, p, -2.10102402082508e-06f);
@@ -109,13 +133,14 @@ __device__ __forceinline__ float gelu_fma(float x) {
   q = __builtin_fmaf(t2, q, -1.68282697438203e-03f);
   q = __builtin_fmaf(t2, q, -7.37332916720468e-03f);
   q = __builtin_fmaf(t2, q, -1.42647390514189e-02f);
-  return (0.5f * x) * (1.0f + p / q);
+  return (0.5f * x) * (1.0f + (FAST ? gelu_div(p, q) : p / q));
 }
 
 // geluScalar (linalg/fastmath.go:9-26): separate roundings.
+template <bool FAST = true>
 __device__ __forceinline__ float gelu_scalar(float x) {
   float e = x * 0.7071067811865476f;
-  e = fmin32(fmax32(e, -4.0f), 4.0f);
+  e = FAST ? gelu_clamp(e) : fmin32(fmax32(e, -4.0f), 4.0f);
   float x2 = e * e;
   float p = x2 * -2.72614225801306e-10f + 2.77068142495902e-08f;
   p = x2 * p + -2.10102402082508e-06f;
@@ -128,7 +153,7 @@ __device__ __forceinline__ float gelu_scalar(float x) {
   q = x2 * q + -1.68282697438203e-03f;
   q = x2 * q + -7.37332916720468e-03f;
   q = x2 * q + -1.42647390514189e-02f;
-  return 0.5f * x * (1.0f + p / q);
+  return 0.5f * x * (1.0f + (FAST ? gelu_div(p, q) : p / q));
 }
 
 // Direct-to-LDS loads (global_load_lds_dwordx4): pointer types, and the
@@ -144,6 +169,31 @@ __device__ __forceinline__ int swz(int row) { return (row >> 1) & 3; }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier for LDS only: this wave's LDS accesses complete
+// (lgkmcnt 0), then s_barrier; the wave's global loads stay in flight
+// (__syncthreads would wait for them too).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt 63, expcnt 7, lgkmcnt 0
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Max of x over each 16-lane row of the wave (DPP row_ror 8, 4, 2, 1):
+// every lane gets its row's max. x must not be NaN.
+__device__ __forceinline__ float row16_max(float x) {
+  int v = __float_as_int(x);
+  v = __float_as_int(__builtin_fmaxf(__int_as_float(v),
+                                     __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false))));
+  v = __float_as_int(__builtin_fmaxf(__int_as_float(v),
+                                     __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false))));
+  v = __float_as_int(__builtin_fmaxf(__int_as_float(v),
+                                     __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x122, 0xF, 0xF, false))));
+  v = __float_as_int(__builtin_fmaxf(__int_as_float(v),
+                                     __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x121, 0xF, 0xF, false))));
+  return __int_as_float(v);
 }
 
 // Max of x over the 32 lanes of each half-wave (lanes 0-31, 32-63) with
@@ -164,6 +214,14 @@ __device__ __forceinline__ float halfwave_max(float x) {
   v = __float_as_int(__builtin_fmaxf(__int_as_float(v),
                                      __int_as_float(__builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false))));
   return __int_as_float(v);
+}
+
+// Max of x over the whole wave, in every lane (DPP within the half-waves,
+// then their two maxima read from lanes 31 and 63). x must not be NaN.
+__device__ __forceinline__ float wave_max(float x) {
+  const int h = __float_as_int(halfwave_max(x));
+  return __builtin_fmaxf(__int_as_float(__builtin_amdgcn_readlane(h, 31)),
+                         __int_as_float(__builtin_amdgcn_readlane(h, 63)));
 }
 
 // Dequantisation of one int8 GEMM result (kernel_vnni_amd64.s:144-200):

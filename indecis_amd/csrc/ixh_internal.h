@@ -25,6 +25,7 @@ struct Tuning {
   int gemm_tile = 0;      // gemm_i8 tiles: 0 128x128/2 stages, 1 256x128/3, 2 128x128/3
   int ln_seg = 1;         // LayerNorm lanes 8/16: 1 segment kernel, 0 whole-row LDS kernel
   int fuse_res = 1;       // residual GEMMs fused with quantizeA of their input and the next LN
+  int fuse_mlp = 1;       // the MLP block (Wi, GeGLU, quantizeA, WoMLP, next LN) as one kernel
 };
 
 // ---- int8 GEMM ----------------------------------------------------------
@@ -114,6 +115,34 @@ struct ResArgs {
 };
 bool gemm_res_supported(int H, int Kp, int Np);
 bool launch_gemm_res(const ResArgs &a, int lanes, hipStream_t s);
+
+// The MLP block in one kernel (mlp_res.hip): X[m][:H] += deq(quantizeA(
+// GeGLU(deq(Aq[m] . Wi^T))) . WoMLP^T), then, with gamma, Q/SA =
+// quantizeA(LayerNorm(X[m], gamma)). Aq/sa and Q/SA may be the same
+// buffers: a workgroup reads its rows before it writes them. Needs (H, I)
+// one of (768, 1152), (256, 512), unpadded, and every gated column in the
+// FMA-form GELU (n_gelu == I); returns false (nothing launched) otherwise.
+struct MlpArgs {
+  const int8_t *Aq;      // [M][ldq] quantised mlp_norm rows (H bytes valid)
+  const float *sa;       // [M] their scales
+  const int8_t *Bi;      // Wi K-blocked [H/32][Npi][32], rows interleaved by 32
+  int Npi;               // 2I
+  const float *sbi, *zci;  // [Npi]
+  const int32_t *c128i;    // [Npi]
+  int n_gelu;            // gated columns below it take the FMA-form GELU (must be I)
+  const int8_t *Bo;      // WoMLP K-blocked [I/32][H][32]
+  const float *sbo, *zco;  // [H]
+  const int32_t *c128o;    // [H]
+  float *X;              // [M][H] residual, updated in place
+  int M, H, I;
+  const float *gamma;    // [H] LayerNorm weight of the new x, or nullptr
+  double eps;
+  int8_t *Q;             // [M][ldq] quantised LayerNorm output
+  int ldq;
+  float *SA;             // [M] its scales
+};
+bool mlp_res_supported(int H, int I, int KpH, int KpI, int Npi);
+bool launch_mlp_res(const MlpArgs &a, int lanes, hipStream_t s);
 
 // ---- host helpers (ixh_api.cpp) ---------------------------------------------
 // Sets the calling thread's ixh_last_error message; returns code.
@@ -206,6 +235,7 @@ void launch_attn_main(const AttnArgs &a, hipStream_t s);
 // res[5] (zeroed by the caller) = {bad simd, bad scalar, max err simd bits,
 // max err scalar bits, undecided}
 void launch_check_exp255(uint32_t lo, uint32_t hi, unsigned long long *res, hipStream_t s);
+void launch_check_gelu(unsigned long long *res, hipStream_t s);
 
 constexpr int kAttnQBlock = 128;  // queries per workgroup (4 waves x 32)
 constexpr int kKeyPad = 64;       // key slots of a sequence are padded to this

@@ -146,3 +146,12 @@ def check_exp255(device=0):
     und = C.c_int64()
     _lib.check(_lib.lib().ixh_check_exp255(device, bad, err, C.byref(und)))
     return int(bad[0]), int(bad[1]), float(err[0]), float(err[1]), int(und.value)
+
+
+def check_gelu(device=0):
+    """Runs the device self-check of the GELU's division and clamp over
+    every float input: returns (bad_fma_form, bad_scalar_form); both must
+    be 0."""
+    bad = (C.c_int64 * 2)()
+    _lib.check(_lib.lib().ixh_check_gelu(device, bad))
+    return int(bad[0]), int(bad[1])

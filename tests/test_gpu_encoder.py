@@ -279,7 +279,29 @@ def test_fused_residual_gemms(shape, lanes):
     if sum(len(s) for s in seqs) % 32 == 0:
         seqs.append(rng.integers(0, cfg.vocab, size=5, dtype=np.int32))
     want, _ = ora.encode_tokens(seqs)
-    for mode, gemm in ((1, 0), (2, 0), (3, 0), (0, 0), (3, 1)):
-        with options(gpu, fuse_res=mode, gemm=gemm):
+    for mode, gemm, mlp in ((1, 0, 1), (1, 0, 0), (2, 0, 0), (3, 0, 0), (0, 0, 0), (3, 1, 0), (2, 0, 1)):
+        with options(gpu, fuse_res=mode, gemm=gemm, fuse_mlp=mlp):
             got = gpu.encode_tokens(seqs)
-        assert f32_bits_equal(got, want), (mode, gemm, mismatch_report(got, want))
+        assert f32_bits_equal(got, want), (mode, gemm, mlp, mismatch_report(got, want))
+
+
+@pytest.mark.parametrize("shape", ["small", "base"])
+def test_fused_mlp_block_rows(shape):
+    """Option fuse_mlp (the default): the MLP block as one kernel (Wi,
+    GeGLU, quantizeA of g, WoMLP, the next LayerNorm + quantizeA;
+    mlp_res.hip), one workgroup per 32 rows, gives the oracle's bits at row
+    counts below, at and around its 32-row blocks, and equals the separate
+    kernels (fuse_mlp 0) on a batch of 4,000 rows."""
+    cfg = small_cfg(layers=2) if shape == "small" else base_cfg(layers=2)
+    w, gpu, ora = model_pair(cfg, seed=73, lanes=8)
+    rng = np.random.default_rng(73)
+    for n in (1, 31, 32, 33, 64, 97):
+        seqs = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32)]
+        got = gpu.encode_tokens(seqs)
+        want, _ = ora.encode_tokens(seqs)
+        assert f32_bits_equal(got, want), (n, mismatch_report(got, want))
+    seqs = ids_uniform_lengths(rng, 16, 150, 350, cfg.vocab)
+    fused = gpu.encode_tokens(seqs)
+    with options(gpu, fuse_mlp=0):
+        separate = gpu.encode_tokens(seqs)
+    assert f32_bits_equal(fused, separate), mismatch_report(fused, separate)
