@@ -29,10 +29,11 @@
 //     128-byte groups), s kept in LDS;
 //  M. WoMLP: wave w owns output columns QC*w .. QC*w + QC - 1 (QC = H/8)
 //     as NB MFMA tiles, weight fragments from [I/32][H][32] PF2 steps
-//     ahead, A fragments from the panel; x of those columns is loaded
-//     before the K loop;
-//  R. dequantisation and the residual add in the MFMA layout, x written
-//     back; the rows staged whole in LDS for the LayerNorm chains; then 16
+//     ahead, A fragments from the panel; meanwhile the block's x rows come
+//     into LDS beside the panel by direct-to-LDS loads;
+//  R. dequantisation and the residual add in the MFMA layout, into the
+//     rows in LDS, written back as 16-byte pieces; the LayerNorm chains
+//     over the same rows; then 16
 //     threads a row: o = ((x - mean) * rstd) * gamma, max |o| by DPP, q8
 //     packed into an int8 row in LDS, stored as 16-byte pieces.
 // Without gamma (the last layer, whose final_norm writes float32) R stops
@@ -63,7 +64,9 @@ struct Shape {
   static constexpr int PF1 = 8;                     // Wi K steps in flight
   static constexpr int ACOL = 32 * (NG - NW);  // g column where the staged input rows sit
   static constexpr int PF2 = 4;                     // WoMLP K steps in flight
-  static constexpr int SMEM = std::max(BM * GLD * 4, BM * XLD * 4 + BM * H);  // g; or x, then its int8 rows
+  // g; or the int8 panel of g (then the output rows) and x
+  static constexpr int SMEM = std::max(BM * GLD * 4, BM * I + BM * XLD * 4);
+  static_assert(BM * H <= BM * I, "output rows fit over the panel");
   static_assert(H % (32 * NW) == 0 && I % 64 == 0 && NG >= NW, "shape");
   // the staged input rows fit in the columns of tiles NG-NW .. NG-1: each
   // is its wave's last tile (tiles are dealt round-robin)
@@ -79,7 +82,8 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
   extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
   float *const gs = (float *)smem;  // W: g [BM][GLD]
   int8_t *const panel = smem;       // Q, M: quantised g [BM][I]
-  float *const xs = (float *)smem;  // R: x [BM][XLD], then bytes [BM][H]
+  float *const xs = (float *)(smem + BM * I);  // M, R: x [BM][XLD], past the panel
+  int8_t *const qs = smem;                     // R: the int8 output rows [BM][H], over the panel
   __shared__ float sa_s[BM], sg_s[BM];
   __shared__ float mean_s[BM], rstd_s[BM];
   __shared__ __attribute__((aligned(16))) float gam_s[LN ? H : 4];  // LayerNorm weight
@@ -190,8 +194,8 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
 #pragma unroll
   for (int r = 0; r < 16; r++) gs[acc_row(r, lane) * GLD + pgc] = gv[r];
 
-  // WoMLP weight fragments of the first PF2 K steps and this wave's x
-  // (independent of g): in flight during Q
+  // WoMLP weight fragments of the first PF2 K steps (independent of g): in
+  // flight during Q
   const auto ors = buf_rsrc(a.Bo, (uint32_t)KT2 * H * 32);
   const int cw = wave * QC;  // first output column of this wave
   auto loadM = [&](int kt, v4i *dst) {
@@ -204,15 +208,6 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
   v4i bm[PF2][NB];
 #pragma unroll
   for (int s = 0; s < PF2; s++) loadM(s, bm[s]);
-  const auto xrs = buf_rsrc(a.X + (size_t)m0 * H, (uint32_t)rows * H * 4);
-  auto roff = [](int r) { return (uint32_t)((8 * (r >> 2) + (r & 3)) * H * 4); };
-  float x[NB][16];
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    const uint32_t vo = (uint32_t)(4 * fh * H + cw + 32 * j + fr) * 4;
-#pragma unroll
-    for (int r = 0; r < 16; r++) x[j][r] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(xrs, vo, roff(r), 0));
-  }
   lds_barrier();  // g complete
 
   // ---- Q. quantizeA of g (int8.go:160-191) ----
@@ -240,6 +235,18 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
     }
     if (qt == 0) sg_s[qr] = s;
     lds_barrier();  // every thread holds its g: the panel goes over it
+    // the block's x rows, 1 KB pieces straight into LDS (xs, past the
+    // panel; g there is dead now), in flight through the rest of Q and the
+    // K loop — issued before the K loop's weight refills, whose waits
+    // (loads retire in order) would otherwise include these (rows past M
+    // load row M-1, never stored)
+    constexpr int CPR = H / 256;  // 1 KB pieces a row
+#pragma unroll
+    for (int c = 0; c < BM * CPR / NW; c++) {
+      const int q = wave + NW * c, row = q / CPR, part = q - row * CPR;
+      const float *src = a.X + (size_t)(m0 + min(row, rows - 1)) * H + 256 * part + 4 * lane;
+      __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(xs + row * XLD + 256 * part), 16, 0, 0);
+    }
     int8_t *prow = panel + qr * I;
 #pragma unroll
     for (int c = 0; c < QV; c++) {
@@ -284,28 +291,30 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
     }
   }
 
-  // ---- R. the reference tile, dequantised, added to x ----
+  // ---- R. the reference tile, dequantised, added to x in LDS ----
+  wait_vmcnt<0>();  // this wave's x pieces landed
+  lds_barrier();    // and every wave's
 #pragma unroll
   for (int j = 0; j < NB; j++) {
-    const uint32_t vo = (uint32_t)(4 * fh * H + cw + 32 * j + fr) * 4;
+    const int col = cw + 32 * j + fr;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const float v = deq(acc[j][r] + c1o[j], zco[j], sbo[j], sg_s[acc_row(r, lane)]);
-      x[j][r] = x[j][r] + v;
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x[j][r]), xrs, vo, roff(r), 0);
+      const int row = acc_row(r, lane);
+      float *xp = xs + row * XLD + col;
+      *xp = *xp + deq(acc[j][r] + c1o[j], zco[j], sbo[j], sg_s[row]);
     }
+  }
+  lds_barrier();
+  // x written back as 16-byte pieces of whole rows
+  for (int idx = tid; idx < BM * (H / 4); idx += 512) {
+    const int row = idx / (H / 4), c4 = idx - row * (H / 4);
+    if (row < rows) *(float4 *)(a.X + (size_t)(m0 + row) * H + 4 * c4) = *(const float4 *)(xs + row * XLD + 4 * c4);
   }
   if constexpr (!LN) return;
 
-  // LayerNorm chains over the staged rows: V > 0: BM*V chains, thread t
+  // LayerNorm chains over the rows in xs: V > 0: BM*V chains, thread t
   // carrying lane partial t % V of row t / V; V 0: one float64 chain a
   // row, threads 0..31
-  lds_barrier();  // every wave is done with the panel
-#pragma unroll
-  for (int j = 0; j < NB; j++)
-#pragma unroll
-    for (int r = 0; r < 16; r++) xs[acc_row(r, lane) * XLD + cw + 32 * j + fr] = x[j][r];
-  lds_barrier();
   constexpr int NCH = V > 0 ? BM * V : BM;
   static_assert(NCH <= 512 && (V == 0 || NCH % 64 == 0), "chains");
   const bool chain = tid < NCH;  // wave-uniform for V > 0
@@ -378,9 +387,8 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
   lds_barrier();
 
   // o = ((x - mean) * rstd) * gamma and quantizeA of the row, from the
-  // staged rows: 16 threads a row (one DPP row), thread qt taking columns
-  // 4(qt + 16c) .. +3; the int8 row goes to qs beside xs
-  int8_t *const qs = (int8_t *)(xs + BM * XLD);  // [BM][H] bytes
+  // rows in xs: 16 threads a row (one DPP row), thread qt taking columns
+  // 4(qt + 16c) .. +3; the int8 row goes to qs
   {
     constexpr int QV = H / 64;
     const int qr = tid >> 4, qt = tid & 15;
