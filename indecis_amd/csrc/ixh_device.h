@@ -4,7 +4,8 @@
 // (the sources are compiled with -ffp-contract=off): __builtin_fmaf where
 // the reference fuses (Go SIMD MulAdd, VFMADD213PS), separate operations
 // where it does not. IEEE division (HIP's default correctly rounded f32
-// divide) and RNE conversions throughout.
+// divide; the GELU's own division, gelu_div, gives the same results on its
+// operand range) and RNE conversions throughout.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
