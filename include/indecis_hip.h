@@ -199,7 +199,8 @@ enum {
   IXH_OPT_FUSE_RES = 7,    /* 1 (default): Wo and WoMLP fused with the quantisation of their
                               input and the next LayerNorm + quantisation; 2: Wo's input
                               streamed in its K loop (attention writes row maxima); 3: also
-                              WoMLP's (the GeGLU epilogue writes them); 0: separate kernels */
+                              WoMLP's (the GeGLU epilogue writes them); 4: Wo on the
+                              whole-row kernel of 8 waves; 0: separate kernels */
   IXH_OPT_FUSE_MLP = 8,    /* 1 (default): Wi, GeGLU, the quantisation of g, WoMLP and the next
                               LayerNorm + quantisation as one kernel (needs FUSE_RES != 0);
                               0: Wi and WoMLP as chosen by FUSE_RES */

@@ -357,7 +357,7 @@ int set_tuning(Tuning &t, int option, int64_t v, bool model_opts) {
     t.ln_seg = (int)v;
     return IXH_OK;
   case IXH_OPT_FUSE_RES:
-    if (v < 0 || v > 3) return bad();
+    if (v < 0 || v > 4) return bad();
     t.fuse_res = (int)v;
     return IXH_OK;
   case IXH_OPT_FUSE_MLP:
@@ -794,7 +794,10 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   // streamed inputs (fuse_res 2: Wo's; 3: Wo's and WoMLP's): attention
   // writes max |ctx| per (row, head), the GeGLU epilogue on gemm_as max
   // |g| per (row, 32 columns); fuse_res 1 quantises whole rows into a panel
-  const bool stream_ctx = fuse_res && tune.fuse_res >= 2 && H == KpH;
+  const bool stream_ctx = fuse_res && (tune.fuse_res == 2 || tune.fuse_res == 3) && H == KpH;
+  // fuse_res 4: Wo on the whole-row kernel of 8 waves (mlp_res.hip)
+  const bool wo8 = fuse_res && tune.fuse_res == 4 && wo_res_supported(H, KpH, m->layers[0].o.np) &&
+                   m->layers[0].o.qk.p;
   float *const cmax = stream_ctx ? w->cmax.as<float>() : nullptr;
   aa.rmax = cmax;
   // the GeGLU maxima exist only where Wi runs on gemm_as (which writes them)
@@ -872,7 +875,25 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
     RUN(global ? "attn_global" : "attn_local", 4.0 * D * nh * pairs,
         dN * 3 * dH + 8 * dN * nh + dN * dH * 4, launch_attn_main(aa, st));
     // x += ctx . Wo^T (infer.go:403), then mlp_norm (infer.go:404-407)
-    if (fuse_res) {
+    if (wo8) {
+      MlpArgs wa{};
+      wa.Af = w->ctx.as<float>();
+      wa.lda = H;
+      wa.Bo = L.o.qk.as<int8_t>();
+      wa.sbo = L.o.sb.as<float>();
+      wa.zco = L.o.zc.as<float>();
+      wa.c128o = L.o.c128.as<int32_t>();
+      wa.X = w->x.as<float>();
+      wa.M = N;
+      wa.H = H;
+      wa.I = H;
+      wa.gamma = L.mlp_norm.as<float>();
+      wa.eps = c.norm_eps;
+      wa.Q = w->xq.as<int8_t>();
+      wa.ldq = KpH;
+      wa.SA = w->sa.as<float>();
+      RUN("gemm_wo_ln", 2 * dN * dH * dH, res_bytes(dH, true), launch_wo_res(wa, c.lanes, st));
+    } else if (fuse_res) {
       const ResArgs r = res(L.o, w->ctx.as<float>(), H, L.mlp_norm.as<float>(), cmax, nh);
       RUN("gemm_wo_ln", 2 * dN * dH * dH, res_bytes(dH, true), launch_gemm_res(r, c.lanes, st));
     } else {

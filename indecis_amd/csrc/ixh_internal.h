@@ -123,6 +123,8 @@ bool launch_gemm_res(const ResArgs &a, int lanes, hipStream_t s);
 // one of (768, 1152), (256, 512), unpadded, and every gated column in the
 // FMA-form GELU (n_gelu == I); returns false (nothing launched) otherwise.
 struct MlpArgs {
+  const float *Af;       // launch_wo_res: [M][lda] float32 ctx rows
+  int lda;
   const int8_t *Aq;      // [M][ldq] quantised mlp_norm rows (H bytes valid)
   const float *sa;       // [M] their scales
   const int8_t *Bi;      // Wi K-blocked [H/32][Npi][32], rows interleaved by 32
@@ -143,6 +145,12 @@ struct MlpArgs {
 };
 bool mlp_res_supported(int H, int I, int KpH, int KpI, int Npi);
 bool launch_mlp_res(const MlpArgs &a, int lanes, hipStream_t s);
+// The same kernel for Wo (mlp_res.hip, WO mode): X[m] += deq(quantizeA(
+// Af[m][:H]) . Wo^T), then Q/SA = quantizeA(LayerNorm(X[m], gamma)); Bo,
+// sbo, zco, c128o are Wo's (K-blocked [H/32][H][32]). Needs H 768 or 256,
+// unpadded, and gamma.
+bool wo_res_supported(int H, int KpH, int Np);
+bool launch_wo_res(const MlpArgs &a, int lanes, hipStream_t s);
 
 // ---- host helpers (ixh_api.cpp) ---------------------------------------------
 // Sets the calling thread's ixh_last_error message; returns code.

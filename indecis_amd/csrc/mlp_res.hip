@@ -74,7 +74,10 @@ struct Shape {
   static_assert(KT1 % PF1 == 0 && KT2 % PF2 == 0, "prefetch depth");
 };
 
-template <int H, int I, int V, bool LN>
+// WO: the kernel for Wo instead (I = H): the block's float32 ctx rows are
+// quantised into the panel (quantizeA, 16 threads a row) in place of W and
+// Q; M and R are the same.
+template <int H, int I, int V, bool LN, bool WO>
 __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
   using S = Shape<H, I>;
   constexpr int KT1 = S::KT1, NG = S::NG, KT2 = S::KT2, NB = S::NB, QC = S::QC;
@@ -94,6 +97,9 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
   const int rows = min(M - m0, BM);
   const uint32_t bvo = (uint32_t)fr * 32 + 16 * fh;  // lane offset in a weight fragment
 
+  if (LN && tid < H / 4) *(float4 *)(gam_s + 4 * tid) = *(const float4 *)(a.gamma + 4 * tid);
+
+  if constexpr (!WO) {
   // ---- W. Wi + GeGLU ----
   // weight fragments of step (k, kt): tile wave + NW k, K step kt
   const int ntile = (NG - wave + NW - 1) / NW;
@@ -119,7 +125,6 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
     }
   }
   if (tid < BM) sa_s[tid] = tid < rows ? a.sa[m0 + tid] : 0.f;
-  if (LN && tid < H / 4) *(float4 *)(gam_s + 4 * tid) = *(const float4 *)(a.gamma + 4 * tid);
   // the first weight fragments, issued after the row loads (which the LDS
   // writes above wait for) so that they stay in flight across the barrier
   v4i bq[PF1][2];
@@ -193,6 +198,7 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
   lds_barrier();  // every wave is done with the staged rows
 #pragma unroll
   for (int r = 0; r < 16; r++) gs[acc_row(r, lane) * GLD + pgc] = gv[r];
+  }  // !WO
 
   // WoMLP weight fragments of the first PF2 K steps (independent of g): in
   // flight during Q
@@ -208,6 +214,48 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
   v4i bm[PF2][NB];
 #pragma unroll
   for (int s = 0; s < PF2; s++) loadM(s, bm[s]);
+  constexpr int CPR = H / 256;  // 1 KB pieces of an x row
+  // the block's x rows, 1 KB pieces straight into LDS (xs, past the panel),
+  // in flight through the rest of Q and the K loop — issued before the K
+  // loop's weight refills, whose waits (loads retire in order) would
+  // otherwise include these (rows past M load row M-1, never stored)
+  auto load_x = [&] {
+#pragma unroll
+    for (int c = 0; c < BM * CPR / NW; c++) {
+      const int q = wave + NW * c, row = q / CPR, part = q - row * CPR;
+      const float *src = a.X + (size_t)(m0 + min(row, rows - 1)) * H + 256 * part + 4 * lane;
+      __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(xs + row * XLD + 256 * part), 16, 0, 0);
+    }
+  };
+  if constexpr (WO) {
+    // ---- Q. quantizeA of the ctx rows (int8.go:160-191) into the panel ----
+    constexpr int QV = H / 64;  // float4 a thread
+    const int qr = tid >> 4, qt = tid & 15;
+    const float *arow = a.Af + (size_t)(m0 + min(qr, rows - 1)) * a.lda;  // rows past M: never stored
+    float4 cv[QV];
+#pragma unroll
+    for (int c = 0; c < QV; c++) cv[c] = *(const float4 *)(arow + 4 * (qt + 16 * c));
+    load_x();
+    float mx = 0.f;
+#pragma unroll
+    for (int c = 0; c < QV; c++)
+      mx = fmax32(mx, fmax32(fmax32(fabsf(cv[c].x), fabsf(cv[c].y)), fmax32(fabsf(cv[c].z), fabsf(cv[c].w))));
+    mx = row16_max(mx);  // the row's 16 threads are one DPP row
+    float s = 0.f, inv = 0.f;
+    if (mx != 0.f) {  // quantizeA: s = max/127, inv = 1/s (int8.go:175-183)
+      s = mx / 127.0f;
+      inv = 1.0f / s;
+    }
+    if (qt == 0) sg_s[qr] = s;
+    int8_t *prow = panel + qr * I;
+#pragma unroll
+    for (int c = 0; c < QV; c++) {
+      const int i = 4 * (qt + 16 * c), ch = i >> 4;
+      const int q0 = q8(cv[c].x, inv), q1 = q8(cv[c].y, inv), q2 = q8(cv[c].z, inv), q3 = q8(cv[c].w, inv);
+      *(int *)(prow + 128 * (ch >> 3) + 16 * ((ch & 7) ^ (qr & 7)) + (i & 15)) =
+          (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+    }
+  } else {
   lds_barrier();  // g complete
 
   // ---- Q. quantizeA of g (int8.go:160-191) ----
@@ -235,18 +283,7 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
     }
     if (qt == 0) sg_s[qr] = s;
     lds_barrier();  // every thread holds its g: the panel goes over it
-    // the block's x rows, 1 KB pieces straight into LDS (xs, past the
-    // panel; g there is dead now), in flight through the rest of Q and the
-    // K loop — issued before the K loop's weight refills, whose waits
-    // (loads retire in order) would otherwise include these (rows past M
-    // load row M-1, never stored)
-    constexpr int CPR = H / 256;  // 1 KB pieces a row
-#pragma unroll
-    for (int c = 0; c < BM * CPR / NW; c++) {
-      const int q = wave + NW * c, row = q / CPR, part = q - row * CPR;
-      const float *src = a.X + (size_t)(m0 + min(row, rows - 1)) * H + 256 * part + 4 * lane;
-      __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(xs + row * XLD + 256 * part), 16, 0, 0);
-    }
+    load_x();       // g past the panel is dead now
     int8_t *prow = panel + qr * I;
 #pragma unroll
     for (int c = 0; c < QV; c++) {
@@ -254,6 +291,7 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
       *(int *)(prow + 128 * (ch >> 3) + 16 * ((ch & 7) ^ (qr & 7)) + (i & 15)) = pk[c];
     }
   }
+  }  // !WO
   lds_barrier();
 
   // ---- M. WoMLP ----
@@ -428,32 +466,32 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
   }
 }
 
-template <int H, int I, int V, bool LN>
+template <int H, int I, int V, bool LN, bool WO>
 void launch_one(const MlpArgs &a, hipStream_t s) {
   constexpr size_t shm = Shape<H, I>::SMEM;
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void *)mlp_res_kernel<H, I, V, LN>,
+    (void)hipFuncSetAttribute((const void *)mlp_res_kernel<H, I, V, LN, WO>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
     attr = true;
   }
-  mlp_res_kernel<H, I, V, LN><<<(a.M + BM - 1) / BM, 512, shm, s>>>(a);
+  mlp_res_kernel<H, I, V, LN, WO><<<(a.M + BM - 1) / BM, 512, shm, s>>>(a);
 }
 
-template <int H, int I, bool LN>
+template <int H, int I, bool LN, bool WO>
 bool launch_v(const MlpArgs &a, int lanes, hipStream_t s) {
   switch (lanes) {
-  case 0: launch_one<H, I, 0, LN>(a, s); return true;
-  case 4: launch_one<H, I, 4, LN>(a, s); return true;
-  case 8: launch_one<H, I, 8, LN>(a, s); return true;
-  case 16: launch_one<H, I, 16, LN>(a, s); return true;
+  case 0: launch_one<H, I, 0, LN, WO>(a, s); return true;
+  case 4: launch_one<H, I, 4, LN, WO>(a, s); return true;
+  case 8: launch_one<H, I, 8, LN, WO>(a, s); return true;
+  case 16: launch_one<H, I, 16, LN, WO>(a, s); return true;
   default: return false;
   }
 }
 
 template <int H, int I>
 bool launch_ln(const MlpArgs &a, int lanes, hipStream_t s) {
-  return a.gamma ? launch_v<H, I, true>(a, lanes, s) : launch_v<H, I, false>(a, lanes, s);
+  return a.gamma ? launch_v<H, I, true, false>(a, lanes, s) : launch_v<H, I, false, false>(a, lanes, s);
 }
 
 // Every float x through both GELU forms, with gelu_div and gelu_clamp
@@ -489,6 +527,16 @@ void launch_check_gelu(unsigned long long *res, hipStream_t s) {
 bool mlp_res_supported(int H, int I, int KpH, int KpI, int Npi) {
   if (KpH != H || KpI != I || Npi != 2 * I) return false;
   return (H == 768 && I == 1152) || (H == 256 && I == 512);
+}
+
+bool wo_res_supported(int H, int KpH, int Np) { return KpH == H && Np == H && (H == 768 || H == 256); }
+
+bool launch_wo_res(const MlpArgs &a, int lanes, hipStream_t s) {
+  using namespace mlp_res_impl;
+  if (a.M <= 0) return true;
+  if (!wo_res_supported(a.H, a.H, a.H) || a.ldq < a.H || a.ldq % 16 != 0 || a.lda % 4 != 0 || !a.gamma) return false;
+  if (a.H == 768) return launch_v<768, 768, true, true>(a, lanes, s);
+  return launch_v<256, 256, true, true>(a, lanes, s);
 }
 
 bool launch_mlp_res(const MlpArgs &a, int lanes, hipStream_t s) {

@@ -267,7 +267,9 @@ def test_fused_residual_gemms(shape, lanes):
     into a whole-row panel first (1, the default) or streamed in the K
     loop from the producers' row maxima (2: Wo's, from attention's maxima
     per head; 3: also WoMLP's, from the GeGLU epilogue's maxima per 32
-    columns), give the separate kernels' bits (0) and the oracle's, for
+    columns), or Wo on the 8-wave whole-row kernel (4, mlp_res.hip), with
+    and without the MLP kernel, give the separate kernels' bits (0) and the
+    oracle's, for
     every lane width of the LayerNorm chains, at both model widths, with
     row counts that leave a partial 32-row block and a last layer without
     LayerNorm; also with Wi on gemm_i8 (option gemm 1: no GeGLU maxima,
@@ -279,7 +281,8 @@ def test_fused_residual_gemms(shape, lanes):
     if sum(len(s) for s in seqs) % 32 == 0:
         seqs.append(rng.integers(0, cfg.vocab, size=5, dtype=np.int32))
     want, _ = ora.encode_tokens(seqs)
-    for mode, gemm, mlp in ((1, 0, 1), (1, 0, 0), (2, 0, 0), (3, 0, 0), (0, 0, 0), (3, 1, 0), (2, 0, 1)):
+    for mode, gemm, mlp in ((1, 0, 1), (1, 0, 0), (2, 0, 0), (3, 0, 0), (0, 0, 0), (3, 1, 0), (2, 0, 1),
+                            (4, 0, 1), (4, 0, 0)):
         with options(gpu, fuse_res=mode, gemm=gemm, fuse_mlp=mlp):
             got = gpu.encode_tokens(seqs)
         assert f32_bits_equal(got, want), (mode, gemm, mlp, mismatch_report(got, want))
