@@ -585,14 +585,17 @@ void run_gemm(int epi, const GemmArgs &g, const Tuning &t, hipStream_t st) {
   launch_gemm(epi, gi, st);
 }
 
-// Parts of a batch of B sequences and N tokens on a model of hidden H (from
-// kSplitTokens tokens on): Tuning::parts when set; else three for a wide
-// model with many sequences to balance (at least 48K tokens, 24 sequences
-// and H 768: cfg4 2% faster than two), else two (three were 1-2% slower on
-// eight 8,192-token sequences, 8% on cfg3's H 256).
+// Parts of a batch (from kSplitTokens tokens on): Tuning::parts when set,
+// else two. With the MLP block as one kernel that fills a CU, three parts
+// were 1.4% slower than two on cfg4 (24.66-24.73 against 24.32-24.38 ms a
+// pass, one box) and four 2%; three were also slower on eight 8,192-token
+// sequences (1-2%) and on cfg3's H 256 (8%).
 int split_parts(const Tuning &t, int N, int B, int H) {
+  (void)N;
+  (void)B;
+  (void)H;
   if (t.parts > 0) return std::min(t.parts, 4);
-  return N >= 48 * 1024 && B >= 24 && H >= 768 ? 3 : 2;
+  return 2;
 }
 
 // What a forward pass issued but has not waited for: its profiling records
