@@ -38,11 +38,16 @@ int fail(int code, const char *fmt, ...) {
   return code;
 }
 
+// A failed call also leaves its error as the thread's last error, which a
+// later LAUNCHCK would report as the failure of an unrelated launch: it is
+// taken back here.
 #define HIPCK(call)                                                                      \
   do {                                                                                   \
     hipError_t e_ = (call);                                                              \
-    if (e_ != hipSuccess)                                                                \
+    if (e_ != hipSuccess) {                                                              \
+      (void)hipGetLastError();                                                           \
       return fail(IXH_EHIP, "modernbert: hip: %s (%s)", hipGetErrorString(e_), #call);   \
+    }                                                                                    \
   } while (0)
 #define LAUNCHCK(what)                                                                   \
   do {                                                                                   \
@@ -611,6 +616,9 @@ struct Pending {
 int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w, hipStream_t st,
             const int32_t *d_ids, const int32_t *offs, int B, const Outputs &out,
             Pending *defer = nullptr) {
+  // an error left by a call outside this pass (the caller's, or one this
+  // library already reported) is not this pass's launch failure
+  (void)hipGetLastError();
   const ixh_config &c = m->cfg;
   const int H = c.hidden, I = c.intermediate, nh = c.heads, D = m->D;
   const int N = offs[B];

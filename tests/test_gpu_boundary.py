@@ -3,7 +3,10 @@ CLS pooling (infer.go:264-273), PackedB8 panel uploads (int8.go:30,
 65-68), a caller's RoPE tables (ropeFor, model.go:256-277), batches over
 the pass size, the decision heads on the device (heads.go:63-74,
 spans.go:369-470) and cfg5's 8,192-key sequences (attention8.go:298-376),
-each against the CPU oracle bit for bit."""
+each against the CPU oracle bit for bit; and a device allocation that
+fails, as a clean error."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -272,4 +275,32 @@ def test_bf16_exact_rows_later_wins():
     got = gpu.encode_tokens(seqs)
     want, _ = ora.encode_tokens(seqs)
     assert f32_bits_equal(got, want), mismatch_report(got, want)
+    gpu.close()
+
+
+def test_failed_allocation_is_a_clean_error():
+    """A device allocation that cannot succeed — the embedding table of a
+    model whose vocabulary needs more bytes than the GPU has — fails with the
+    library's HIP error and message (nothing is launched, the host table is
+    not read), and leaves nothing behind: encodes on a working model before
+    and after it give the oracle's bits."""
+    import dataclasses
+    import torch
+    cfg = small_cfg(layers=1)
+    w, gpu, ora = _pair(cfg, seed=49)
+    rng = np.random.default_rng(49)
+    seqs = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32) for n in (40, 7)]
+    want, _ = ora.encode_tokens(seqs)
+    assert f32_bits_equal(gpu.encode_tokens(seqs), want)
+    big = dataclasses.replace(cfg, vocab=700_000_000)
+    need = 4 * big.vocab * big.hidden
+    total = torch.cuda.get_device_properties(0).total_memory
+    if need <= 2 * total:
+        pytest.skip(f"the device holds {total} bytes: the table would fit")
+    huge = Model(None, cfg=big, lanes=8)
+    tiny = np.zeros(16, np.float32)  # never read: the allocation fails first
+    with pytest.raises(_lib.IxhError, match="out of memory|hip:"):
+        _lib.check(_lib.lib().ixh_model_set_embeddings_f32(huge._h, tiny.ctypes.data_as(C.c_void_p)))
+    huge.close()
+    assert f32_bits_equal(gpu.encode_tokens(seqs), want)
     gpu.close()
