@@ -645,18 +645,35 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
                    [&](int x, int y) { return offs[x + 1] - offs[x] > offs[y + 1] - offs[y]; });
   // qkv_fused 0: QKV GEMM and attention prologue as two kernels (tests, timing)
   const bool fused = T <= kQkvSeqMax && tune.qkv_fused != 0;
+  // the residual GEMMs fused with quantizeA of their input and the next
+  // LayerNorm + quantizeA (gemm_res.hip), where the shapes allow it
+  const bool fuse_res = tune.fuse_res != 0 && gemm_res_supported(H, KpH, m->layers[0].o.np) &&
+                        gemm_res_supported(H, KpI, m->layers[0].omlp.np);
+  // streamed inputs (fuse_res 2: Wo's; 3: Wo's and WoMLP's): attention
+  // writes max |ctx| per (row, head), the GeGLU epilogue on gemm_as max
+  // |g| per (row, 32 columns); fuse_res 1 quantises whole rows into a panel
+  const bool stream_ctx = fuse_res && (tune.fuse_res == 2 || tune.fuse_res == 3) && H == KpH;
+  // fuse_res 4: Wo on the whole-row kernel of 8 waves (mlp_res.hip)
+  const bool wo8 = fuse_res && tune.fuse_res == 4 && wo_res_supported(H, KpH, m->layers[0].o.np) &&
+                   m->layers[0].o.qk.p;
+  // the whole MLP block as one kernel (mlp_res.hip), where the shapes allow
+  // it; it takes the mlp_norm output quantised by the fused Wo kernel
+  const bool fuse_mlp = fuse_res && tune.fuse_mlp != 0 &&
+                        mlp_res_supported(H, I, KpH, KpI, m->layers[0].i.np) && m->layers[0].i.qk.p &&
+                        m->layers[0].omlp.qk.p && gelu_fma_cols(I, c.lanes) == I;
 
   int rc;
   const size_t ntab = 2 * (size_t)(B + 1) + blocks.size() + B;
   if ((rc = w->tabs.ensure(4 * ntab)) || (rc = w->pos.ensure(4 * (size_t)N)) ||
       (rc = w->x.ensure(4 * (size_t)N * H)) || (rc = w->xn.ensure(4 * (size_t)N * H)) ||
-      (rc = w->qkv.ensure(4 * (size_t)N * 3 * H)) || (rc = w->xq.ensure((size_t)N * ldq)) ||
+      (!fused && (rc = w->qkv.ensure(4 * (size_t)N * 3 * H))) || (rc = w->xq.ensure((size_t)N * ldq)) ||
       (rc = w->sa.ensure(4 * (size_t)N)) || (rc = w->qq.ensure((size_t)N * H)) ||
       (rc = w->sq.ensure(4 * (size_t)N * nh)) || (rc = w->kp.ensure((size_t)nh * Npad * D)) ||
       (rc = w->ks.ensure(4 * (size_t)nh * Npad)) || (rc = w->vt.ensure((size_t)nh * D * Npad)) ||
       (rc = w->vs.ensure(3 * 4 * (size_t)B * nh * D)) || (rc = w->ctx.ensure(4 * (size_t)N * H)) ||
-      (rc = w->g.ensure(4 * (size_t)N * I)) || (rc = w->cmax.ensure(4 * (size_t)N * nh)) ||
-      (rc = w->gmax.ensure(4 * (size_t)N * (I / 32))))
+      (!fuse_mlp && (rc = w->g.ensure(4 * (size_t)N * I))) ||
+      (stream_ctx && (rc = w->cmax.ensure(4 * (size_t)N * nh))) ||
+      (stream_ctx && (rc = w->gmax.ensure(4 * (size_t)N * (I / 32)))))
     return rc;
 
   // small host-built tables through pinned memory, one copy
@@ -798,17 +815,6 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   ln.seg = tune.ln_seg;
   const double ln_bytes = dN * (4 * dH + dH + 4);
 
-  // the residual GEMMs fused with quantizeA of their input and the next
-  // LayerNorm + quantizeA (gemm_res.hip), where the shapes allow it
-  const bool fuse_res = tune.fuse_res != 0 && gemm_res_supported(H, KpH, m->layers[0].o.np) &&
-                        gemm_res_supported(H, KpI, m->layers[0].omlp.np);
-  // streamed inputs (fuse_res 2: Wo's; 3: Wo's and WoMLP's): attention
-  // writes max |ctx| per (row, head), the GeGLU epilogue on gemm_as max
-  // |g| per (row, 32 columns); fuse_res 1 quantises whole rows into a panel
-  const bool stream_ctx = fuse_res && (tune.fuse_res == 2 || tune.fuse_res == 3) && H == KpH;
-  // fuse_res 4: Wo on the whole-row kernel of 8 waves (mlp_res.hip)
-  const bool wo8 = fuse_res && tune.fuse_res == 4 && wo_res_supported(H, KpH, m->layers[0].o.np) &&
-                   m->layers[0].o.qk.p;
   float *const cmax = stream_ctx ? w->cmax.as<float>() : nullptr;
   aa.rmax = cmax;
   // the GeGLU maxima exist only where Wi runs on gemm_as (which writes them)
@@ -816,11 +822,6 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   if (stream_ctx && tune.fuse_res == 3 && I == KpI && tune.gemm != 1 &&
       gemm_as_supported(gemm(EPI_GEGLU, m->layers[0].i, KpH, nullptr, I, I)))
     gmax = w->gmax.as<float>();
-  // the whole MLP block as one kernel (mlp_res.hip), where the shapes allow
-  // it; it takes the mlp_norm output quantised by the fused Wo kernel
-  const bool fuse_mlp = fuse_res && tune.fuse_mlp != 0 &&
-                        mlp_res_supported(H, I, KpH, KpI, m->layers[0].i.np) && m->layers[0].i.qk.p &&
-                        m->layers[0].omlp.qk.p && gelu_fma_cols(I, c.lanes) == I;
   auto res = [&](const Mat &M, const float *A, int K, const float *gamma, const float *amax, int P) {
     ResArgs r{};
     r.A = A;
