@@ -380,49 +380,65 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   const float *ksglob = a.ks + (size_t)h * a.Npad + slot0;
   const int8_t *vglob = a.vt + (size_t)h * D * a.Npad + slot0;
 
-  auto stage_k = [&](int c0) {
-    for (int e = tid; e < CHUNK * 4; e += 256) {
-      const int key = e >> 2, part = e & 3;
-      v4i w = {0, 0, 0, 0};
-      if (c0 + key < npad) w = *(const v4i *)(kglob + (size_t)(c0 + key) * D + 16 * part);
-      *(v4i *)&Ks[key * KS + 16 * part] = w;
-    }
-    for (int e = tid; e < CHUNK; e += 256) kss[e] = c0 + e < npad ? ksglob[c0 + e] : 0.f;
-  };
-  // V^T with the 8 dwords of each 32-key group permuted so that lane half
-  // hf reads the keys 8*(b/4) + 4*hf + b%4 (the S^T accumulator rows) as
-  // 16 contiguous bytes.
-  auto stage_v = [&](int c0) {
-    for (int e = tid; e < D * (CHUNK / 32); e += 256) {
-      const int d = e / (CHUNK / 32), g = e % (CHUNK / 32);
-      int w[8];
-      if (c0 + 32 * g < npad) {
-        const v4i lo = *(const v4i *)(vglob + (size_t)d * a.Npad + c0 + 32 * g);
-        const v4i hi = *(const v4i *)(vglob + (size_t)d * a.Npad + c0 + 32 * g + 16);
-        w[0] = lo[0]; w[1] = lo[1]; w[2] = lo[2]; w[3] = lo[3];
-        w[4] = hi[0]; w[5] = hi[1]; w[6] = hi[2]; w[7] = hi[3];
-      } else {
+  // Stage the chunk of keys c0 .. c0+CHUNK-1: K rows and their scales,
+  // and with with_v V^T with the 8 dwords of each 32-key group permuted so
+  // that lane half hf reads the keys 8*(b/4) + 4*hf + b%4 (the S^T
+  // accumulator rows) as 16 contiguous bytes, plus each group's sum of V
+  // per dimension. Every global load of the thread is issued before the
+  // first LDS write, so the staging waits on memory once. Buffer loads:
+  // keys past the sequence's slots read 0 (V^T rows continue into the next
+  // sequence's slots, so those loads get an offset past the range).
+  static_assert(CHUNK == 256, "one key scale a thread (256 threads)");
+  constexpr int NKP = CHUNK * 4 / 256;         // 16-byte K pieces a thread
+  constexpr int NVG = D * (CHUNK / 32) / 256;  // V (dimension, group) items a thread
+  const auto krs = buf_rsrc(kglob, (uint32_t)npad * D);
+  const auto ksrs = buf_rsrc(ksglob, (uint32_t)npad * 4);
+  const auto vrs = buf_rsrc(vglob, (uint32_t)((D - 1) * a.Npad + npad));
+  auto stage = [&](int c0, bool with_v) {
+    v4i kw[NKP], vlo[NVG], vhi[NVG];
 #pragma unroll
-        for (int u = 0; u < 8; u++) w[u] = 0;
+    for (int i = 0; i < NKP; i++)
+      kw[i] = __builtin_amdgcn_raw_buffer_load_b128(krs, (uint32_t)((c0 + (tid >> 2) + 64 * i) * D + 16 * (tid & 3)), 0, 0);
+    const float kv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ksrs, (uint32_t)(c0 + tid) * 4, 0, 0));
+    if (with_v) {
+#pragma unroll
+      for (int i = 0; i < NVG; i++) {
+        const int e = tid + 256 * i, d = e / (CHUNK / 32), g = e % (CHUNK / 32);
+        const uint32_t off = c0 + 32 * g < npad ? (uint32_t)(d * a.Npad + c0 + 32 * g) : 0x7fffffe0u;
+        vlo[i] = __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0);
+        vhi[i] = __builtin_amdgcn_raw_buffer_load_b128(vrs, off + 16, 0, 0);
       }
-      v4i o0 = {w[0], w[2], w[4], w[6]}, o1 = {w[1], w[3], w[5], w[7]};
-      *(v4i *)&Vs[d * VS + 32 * g] = o0;
-      *(v4i *)&Vs[d * VS + 32 * g + 16] = o1;
-      int sum = 0;
+    }
 #pragma unroll
-      for (int u = 0; u < 8; u++) sum = __builtin_amdgcn_sdot4(w[u], 0x01010101, sum, false);
-      vpre[g][d] = sum;
+    for (int i = 0; i < NKP; i++) *(v4i *)&Ks[((tid >> 2) + 64 * i) * KS + 16 * (tid & 3)] = kw[i];
+    kss[tid] = kv;
+    if (with_v) {
+#pragma unroll
+      for (int i = 0; i < NVG; i++) {
+        const int e = tid + 256 * i, d = e / (CHUNK / 32), g = e % (CHUNK / 32);
+        const int w[8] = {vlo[i][0], vlo[i][1], vlo[i][2], vlo[i][3], vhi[i][0], vhi[i][1], vhi[i][2], vhi[i][3]};
+        const v4i o0 = {w[0], w[2], w[4], w[6]}, o1 = {w[1], w[3], w[5], w[7]};
+        *(v4i *)&Vs[d * VS + 32 * g] = o0;
+        *(v4i *)&Vs[d * VS + 32 * g + 16] = o1;
+        int sum = 0;
+#pragma unroll
+        for (int u = 0; u < 8; u++) sum = __builtin_amdgcn_sdot4(w[u], 0x01010101, sum, false);
+        vpre[g][d] = sum;
+      }
     }
   };
-  // after the barrier that follows stage_v: group sums -> prefix sums
+  // after the barrier that follows stage_v: group sums -> prefix sums (the
+  // group sums read together, then written: one wait on LDS, not one a
+  // group)
   auto prefix_v = [&] {
     if (tid < D) {
-      int acc = 0;
+      int gsum[CHUNK / 32];
 #pragma unroll
-      for (int g = 0; g < CHUNK / 32; g++) {
-        acc += vpre[g][tid];
-        vpre[g][tid] = acc;
-      }
+      for (int g = 0; g < CHUNK / 32; g++) gsum[g] = vpre[g][tid];
+#pragma unroll
+      for (int g = 1; g < CHUNK / 32; g++) gsum[g] += gsum[g - 1];
+#pragma unroll
+      for (int g = 0; g < CHUNK / 32; g++) vpre[g][tid] = gsum[g];
     }
     __syncthreads();
   };
@@ -456,8 +472,7 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   float m = -__builtin_huge_valf();
   for (int c0 = bk0; c0 < bk1; c0 += CHUNK) {
     __syncthreads();
-    stage_k(c0);
-    if (one_chunk) stage_v(c0);
+    stage(c0, one_chunk);
     __syncthreads();
     if (one_chunk) prefix_v();
     const int t0 = max(wt0, c0 / 32), t1 = min(wt1, (c0 + CHUNK) / 32);
@@ -497,8 +512,7 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   for (int c0 = bk0; c0 < bk1; c0 += CHUNK) {
     if (!one_chunk) {
       __syncthreads();
-      stage_k(c0);
-      stage_v(c0);
+      stage(c0, true);
       __syncthreads();
       prefix_v();
     }

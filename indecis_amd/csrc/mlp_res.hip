@@ -332,21 +332,41 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
   // ---- R. the reference tile, dequantised, added to x in LDS ----
   wait_vmcnt<0>();  // this wave's x pieces landed
   lds_barrier();    // and every wave's
+  {
+    // every read issued before the first write: the compiler cannot tell
+    // xs from the row scales, so read-add-write per element would wait on
+    // LDS once per element
+    float sgv[16], xv[NB][16];
 #pragma unroll
-  for (int j = 0; j < NB; j++) {
-    const int col = cw + 32 * j + fr;
+    for (int r = 0; r < 16; r++) sgv[r] = sg_s[acc_row(r, lane)];
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = acc_row(r, lane);
-      float *xp = xs + row * XLD + col;
-      *xp = *xp + deq(acc[j][r] + c1o[j], zco[j], sbo[j], sg_s[row]);
-    }
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) xv[j][r] = xs[acc_row(r, lane) * XLD + cw + 32 * j + fr];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        xs[acc_row(r, lane) * XLD + cw + 32 * j + fr] = xv[j][r] + deq(acc[j][r] + c1o[j], zco[j], sbo[j], sgv[r]);
   }
   lds_barrier();
-  // x written back as 16-byte pieces of whole rows
-  for (int idx = tid; idx < BM * (H / 4); idx += 512) {
-    const int row = idx / (H / 4), c4 = idx - row * (H / 4);
-    if (row < rows) *(float4 *)(a.X + (size_t)(m0 + row) * H + 4 * c4) = *(const float4 *)(xs + row * XLD + 4 * c4);
+  // x written back as 16-byte pieces of whole rows, every LDS read issued
+  // before the first store
+  {
+    constexpr int WB = BM * (H / 4) / 512;  // pieces a thread
+    static_assert(BM * (H / 4) % 512 == 0, "write-back");
+    float4 wv[WB];
+#pragma unroll
+    for (int u = 0; u < WB; u++) {
+      const int idx = tid + 512 * u, row = idx / (H / 4), c4 = idx - row * (H / 4);
+      wv[u] = *(const float4 *)(xs + row * XLD + 4 * c4);
+    }
+#pragma unroll
+    for (int u = 0; u < WB; u++) {
+      const int idx = tid + 512 * u, row = idx / (H / 4), c4 = idx - row * (H / 4);
+      if (row < rows) *(float4 *)(a.X + (size_t)(m0 + row) * H + 4 * c4) = wv[u];
+    }
   }
   if constexpr (!LN) return;
 
