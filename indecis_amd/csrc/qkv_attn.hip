@@ -80,6 +80,7 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
   const int b = order[si];
   const int part = (k % per_seq) / hgroups, h0 = NH * ((k % per_seq) % hgroups), h = h0 + hf;
   const int base = a.offs[b], n = a.offs[b + 1] - base;
+  const int slot0 = a.padoff[b];  // the sequence's first key slot (K and V outputs)
   const int npad = (n + kKeyPad - 1) / kKeyPad * kKeyPad;
   const int nb = npad / 32;            // 32-row blocks stored (even, at most 16)
   const int nbc = (n + 31) / 32;       // blocks computed: a block past n is all zeros
@@ -89,7 +90,20 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
     if (part == 2 && tidh < D) a.vs[((size_t)b * a.nh + h) * D + tidh] = 0.f;
     return;
   }
-  for (int t = tid; t < 32 * nb; t += 512 * NH) sa_s[t] = g.sa[base + min(t, n - 1)];
+  // Loads the K loop does not need, issued before its first stage (loads
+  // retire in order, so the loop's first wait covers them): the row scales
+  // (stored to LDS after the loop) and this lane's column constants.
+  static_assert(SEQ_MAX <= 512, "one row scale a thread");
+  const float sa_v = tid < 32 * nb ? g.sa[base + min(tid, n - 1)] : 0.f;
+  float zc[2], sb[2];
+  int c128[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int nc = col0 + 32 * j + fr;
+    zc[j] = g.zc[nc];
+    sb[j] = g.sb[nc];
+    c128[j] = g.c128[nc];
+  }
 
   // ---- int8 GEMM of the sequence's rows by the head's 64 weight rows ----
   // Stage chunks of 16 rows x 64 bytes (one wave instruction each): A
@@ -169,19 +183,11 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
       }
     }
   }
-  __syncthreads();  // the ring is no longer read
+  if (tid < 32 * nb) sa_s[tid] = sa_v;
+  __syncthreads();  // the ring is no longer read; the row scales are in LDS
 
   // ---- dequantisation (and RoPE on Q and K) in the MFMA layout ----
   // lane: columns fr and 32 + fr of the head, rows 32 rb + acc_row(r)
-  float zc[2], sb[2];
-  int c128[2];
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int nc = col0 + 32 * j + fr;
-    zc[j] = g.zc[nc];
-    sb[j] = g.sb[nc];
-    c128[j] = g.c128[nc];
-  }
   float v[2][2][16];
 #pragma unroll
   for (int i = 0; i < 2; i++) {
@@ -255,7 +261,7 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
     __syncthreads();
     const float vi0 = stat_s[hf][fr], vi1 = stat_s[hf][32 + fr];
     int8_t *vt_s = smem + wave * (D * VT_LD);  // [64 dims][32 keys] of this wave's block
-    int8_t *vt = a.vt + (size_t)h * D * a.Npad + a.padoff[b];
+    int8_t *vt = a.vt + (size_t)h * D * a.Npad + slot0;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int rb = wv + 8 * i;
@@ -338,8 +344,8 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
   // 32, half (lane / 16) % 2), K centred first (quantRowAVX2 without the
   // flip, attention8.go:240-251), Q as Attn8.Prepare quantises queries
   // (attention8.go:211-220).
-  int8_t *kp = a.kp + ((size_t)h * a.Npad + a.padoff[b]) * D;
-  float *ks = a.ks + (size_t)h * a.Npad + a.padoff[b];
+  int8_t *kp = a.kp + ((size_t)h * a.Npad + slot0) * D;
+  float *ks = a.ks + (size_t)h * a.Npad + slot0;
   const int hh = (lane >> 4) & 1;
   const int lr = 32 * wv + 16 * (lane >> 5) + (lane & 15);
   auto quant_round = [&](int t) {
