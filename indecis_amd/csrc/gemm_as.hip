@@ -238,25 +238,12 @@ __global__ __launch_bounds__(256, 2) void gemm_as_kernel(GemmArgs a, int units, 
   }
 }
 
-int num_cus() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      n = v;
-    else
-      n = 256;
-  }
-  return n;
-}
-
 template <int MB, int KT, int EPI>
 void launch_kt(const GemmArgs &a, hipStream_t s) {
   constexpr int BM = 32 * MB;
   const int nchunk = a.Np / CHUNK;
   const int units = ((a.M + BM - 1) / BM) * nchunk;
-  int G = std::min(units, 2 * num_cus());
+  int G = std::min(units, 2 * device_cus());
   G = std::max(NXCD, G / NXCD * NXCD);
   const size_t shm = (size_t)BM * 32 * KT;
   static bool attr = false;

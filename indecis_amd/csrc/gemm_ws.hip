@@ -264,24 +264,11 @@ __global__ __launch_bounds__(512) void gemm_ws_kernel(GemmArgs a, int units, int
   }
 }
 
-int num_cus() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      n = v;
-    else
-      n = 256;
-  }
-  return n;
-}
-
 template <int KT, int EPI>
 void launch_kt(const GemmArgs &a, hipStream_t s) {
   const int nchunk = a.Np / CHUNK;
   const int units = ((a.M + BM - 1) / BM) * nchunk;
-  int G = std::min(units, num_cus());
+  int G = std::min(units, device_cus());
   G = std::max(NXCD, G / NXCD * NXCD);
   const size_t shm = (size_t)BM * 32 * KT + HAND_BYTES;
   static bool attr = false;

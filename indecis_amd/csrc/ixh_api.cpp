@@ -1242,6 +1242,24 @@ int set_error(int code, const char *msg) {
   g_err = msg;
   return code;
 }
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::atomic<int> &c = cache[dev & 63];
+  int n = c.load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      n = 256;
+    }
+    c.store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 void model_config(const ixh_model *m, ixh_config *out) { *out = m->cfg; }
 }  // namespace ixh
 

@@ -28,6 +28,10 @@ struct Tuning {
   int fuse_mlp = 1;       // the MLP block (Wi, GeGLU, quantizeA, WoMLP, next LN) as one kernel
 };
 
+// Compute units of the current device (cached per device; 256 if the query
+// fails), for grids of resident workgroups.
+int device_cus();
+
 // ---- int8 GEMM ----------------------------------------------------------
 // C = epilogue(A . B^T): A int8 [M][lda] (signed activations, zero
 // padding to Kp), B int8 [Np][ldb] (weights, one row per output channel,

@@ -583,10 +583,9 @@ void launch_resident(Kern kern, int work, int threads, const RowArgs &a, hipStre
   (void)hipGetDevice(&dev);
   int &n = resident[dev & 63];
   if (n == 0) {
-    int cus = 0, per_cu = 0;
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    int per_cu = 0;
     (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)kern, threads, 0);
-    n = std::max(1, cus * per_cu);
+    n = std::max(1, device_cus() * per_cu);
   }
   kern<<<std::min(work, n), threads, 0, s>>>(a);
 }
