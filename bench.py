@@ -344,6 +344,41 @@ def tokenize(np, args):
     }), flush=True)
 
 
+def vendor_gemm(args):
+    """The vendor int8 GEMM on the encoder's GEMM shapes, for reference:
+    torch._int_mm (hipBLASLt) with a plain int32 output, and the same
+    shapes in bf16 (torch.matmul), M = the cfg4 batch's 73,621 tokens.
+    These do only the GEMM; the library's kernels also dequantise, apply
+    the epilogues, the residual, the LayerNorm and the quantisation."""
+    import torch
+    torch.cuda.set_device(0)
+    M = 73621
+    res = {}
+    for K, N, name in ((768, 2304, "qkv, wi"), (768, 768, "wo"), (1152, 768, "womlp")):
+        a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda")
+        b = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda").t()
+        a16 = torch.randn(M, K, dtype=torch.bfloat16, device="cuda")
+        b16 = torch.randn(N, K, dtype=torch.bfloat16, device="cuda").t().contiguous()
+        for label, fn, peak in (("int8", lambda: torch._int_mm(a, b), PEAK_INT8_OPS),
+                                ("bf16", lambda: a16 @ b16, 2.5e15)):
+            for _ in range(args.warmup):
+                fn()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(args.steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / args.steps
+            ops = 2.0 * M * N * K
+            res[f"{name} K{K} N{N} {label}"] = {"us": round(us, 1), "T_per_s": round(ops / us / 1e6, 1),
+                                                "frac_of_dense_peak": round(ops / (us / 1e6) / peak, 4)}
+    print(json.dumps({"vendor_gemm": res, "M": M, "steps": args.steps, "int8_peak": PEAK_INT8_OPS,
+                      "bf16_peak": 2.5e15}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -369,6 +404,8 @@ def main():
     ap.add_argument("--inputs", type=int, default=8192, help="inputs (--decide)")
     ap.add_argument("--decide-lo", type=int, default=8)
     ap.add_argument("--decide-hi", type=int, default=256)
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="instead: the vendor int8 and bf16 GEMMs (torch) on the encoder's GEMM shapes")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -376,6 +413,9 @@ def main():
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
         sys.exit(2)
 
+    if args.vendor_gemm:
+        vendor_gemm(args)
+        return
     import numpy as np
     if args.tokenize:
         tokenize(np, args)
