@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   float *const xs = (float *)(smem + PANEL);         // [BM][XLD], then [BM][H] bytes
   __shared__ float sa_s[BM];
   __shared__ float red_s[4][BM];
-  __shared__ float mean_s[BM], rstd_s[BM];
+  __shared__ float mean_s[BM], rstd_s[BM], inv_s[BM];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fh = lane >> 5;
@@ -363,19 +363,22 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
     if (fr == 16) red_s[wave][acc_row(r, lane)] = mx[r];
   }
   __syncthreads();
+  // the row's scale and its inverse, once a row (quantizeA: s = max/127,
+  // inv = 1/s, int8.go:175-183)
+  if (tid < BM) {
+    const float m = fmax32(fmax32(red_s[0][tid], red_s[1][tid]), fmax32(red_s[2][tid], red_s[3][tid]));
+    const float sc = m != 0.f ? m / 127.0f : 0.f;
+    inv_s[tid] = m != 0.f ? 1.0f / sc : 0.f;
+    if (m0 + tid < M) a.SA[m0 + tid] = sc;
+  }
+  __syncthreads();
   int8_t *const qs = (int8_t *)xs;  // [BM][H] bytes
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     const int row = acc_row(r, lane);
-    const float m = fmax32(fmax32(red_s[0][row], red_s[1][row]), fmax32(red_s[2][row], red_s[3][row]));
-    float inv = 0.f;
-    if (m != 0.f) inv = 1.0f / (m / 127.0f);
+    const float inv = inv_s[row];
 #pragma unroll
     for (int j = 0; j < NB; j++) qs[row * H + cb + 32 * j + fr] = (int8_t)q8(x[j][r], inv);
-  }
-  if (tid < BM && m0 + tid < M) {
-    const float m = fmax32(fmax32(red_s[0][tid], red_s[1][tid]), fmax32(red_s[2][tid], red_s[3][tid]));
-    a.SA[m0 + tid] = m != 0.f ? m / 127.0f : 0.f;
   }
   __syncthreads();
   constexpr int C16 = H / 16;  // 16-byte pieces of a row
