@@ -4,8 +4,8 @@
 // (the sources are compiled with -ffp-contract=off): __builtin_fmaf where
 // the reference fuses (Go SIMD MulAdd, VFMADD213PS), separate operations
 // where it does not. IEEE division (HIP's default correctly rounded f32
-// divide; the GELU's own division, gelu_div, gives the same results on its
-// operand range) and RNE conversions throughout.
+// divide; the GELU's own division, gelu_div, gives the same GELU results
+// on every input) and RNE conversions throughout.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -94,20 +94,20 @@ __device__ __forceinline__ float exp255_fast(float v) {
   return __builtin_amdgcn_exp2f(__builtin_fmaf(v, 1.44269504088896341f, 7.99435343685885793f));
 }
 
-// p / q for the GELU's rational erf, round to nearest: Markstein's
-// FMA-based division (the reciprocal refined by one Newton step, the
-// quotient corrected by two exact remainders). Here q, the denominator
-// polynomial on t*t in [0, 16], lies in [-2.4, -0.0142] and |p| <= |q|, so
-// no operand needs the range scaling of the general IEEE sequence;
-// ixh_check_gelu verifies, for every float input of both GELU forms, that
-// the GELU result equals the one with IEEE division.
+// p / q for the GELU's rational erf: the hardware reciprocal (v_rcp_f32)
+// times p, corrected once by the exact remainder fma(-q, y, p) (Markstein's
+// FMA-based division, one step). Here q, the denominator polynomial on t*t
+// in [0, 16], lies in [-2.4, -0.0142] and |p| <= |q|, so no operand needs
+// the range scaling of the general IEEE sequence. The quotient may differ
+// from the correctly rounded p / q in its last bit; the GELU result
+// 0.5x(1 + p/q) does not: ixh_check_gelu verifies, for every float input of
+// both GELU forms, that it equals the GELU with IEEE division (a refined
+// reciprocal and a second correction change none of those results; with no
+// correction about 15 million inputs differ).
 __device__ __forceinline__ float gelu_div(float p, float q) {
-  float r = __builtin_amdgcn_rcpf(q);
-  r = __builtin_fmaf(__builtin_fmaf(-q, r, 1.0f), r, r);
-  float y = p * r;
-  y = __builtin_fmaf(__builtin_fmaf(-q, y, p), r, y);
-  y = __builtin_fmaf(__builtin_fmaf(-q, y, p), r, y);
-  return y;
+  const float r = __builtin_amdgcn_rcpf(q);
+  const float y = p * r;
+  return __builtin_fmaf(__builtin_fmaf(-q, y, p), r, y);
 }
 
 // clamp of the GELU argument to [-4, 4] (VMAXPS/VMINPS in the reference):

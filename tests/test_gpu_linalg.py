@@ -309,10 +309,11 @@ def test_exp255_shortcut_every_float():
 
 
 def test_gelu_division_every_float():
-    """The kernels' GELU divides with Markstein's FMA sequence (a refined
-    reciprocal, two exact-remainder corrections) and clamps with v_med3
-    instead of IEEE division and compare-select. Over all 2^32 float inputs
-    both GELU forms (geluMulAVX2's FMA form, geluScalar; gelu_amd64.s:173-195,
-    fastmath.go:9-26) must give the IEEE-division result in every bit."""
+    """The kernels' GELU divides with the hardware reciprocal and one
+    exact-remainder FMA correction (Markstein's method, one step) and clamps
+    with v_med3 instead of IEEE division and compare-select. Over all 2^32
+    float inputs both GELU forms (geluMulAVX2's FMA form, geluScalar;
+    gelu_amd64.s:173-195, fastmath.go:9-26) must give the IEEE-division
+    result in every bit."""
     bad_fma, bad_scalar = linalg.check_gelu()
     assert bad_fma == 0 and bad_scalar == 0, (bad_fma, bad_scalar)
