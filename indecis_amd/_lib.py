@@ -36,10 +36,11 @@ NORM_EMB, NORM_ATTN, NORM_MLP, NORM_FINAL = range(4)
 LAYOUT_ROWS, LAYOUT_PANELS = 0, 1
 OUT_POOLED, OUT_TOKENS = 0, 1
 (OPT_PARTS, OPT_PASS_TOKENS, OPT_QKV_FUSED, OPT_QKV_HEADS, OPT_GEMM, OPT_GEMM_TILE,
- OPT_LN_SEG, OPT_FUSE_RES, OPT_FUSE_MLP) = range(9)
+ OPT_LN_SEG, OPT_FUSE_RES, OPT_FUSE_MLP, OPT_QKV_KBLOCK) = range(10)
 OPTIONS = {"parts": OPT_PARTS, "pass_tokens": OPT_PASS_TOKENS, "qkv_fused": OPT_QKV_FUSED,
            "qkv_heads": OPT_QKV_HEADS, "gemm": OPT_GEMM, "gemm_tile": OPT_GEMM_TILE,
-           "ln_seg": OPT_LN_SEG, "fuse_res": OPT_FUSE_RES, "fuse_mlp": OPT_FUSE_MLP}
+           "ln_seg": OPT_LN_SEG, "fuse_res": OPT_FUSE_RES, "fuse_mlp": OPT_FUSE_MLP,
+           "qkv_kblock": OPT_QKV_KBLOCK}
 
 
 class IxhError(RuntimeError):

@@ -255,7 +255,7 @@ struct Workspace {
   hipStream_t stream = nullptr;
   // tabs: the pass's small host-built tables, one copy: offs [B+1], padoff
   // [B+1], blocks [2 nblocks], sequence order [B]
-  DevBuf ids, tabs, pos, x, xn, qkv, xq, sa, qq, sq, kp, ks, vt, vs, ctx, g, pooled, flag;
+  DevBuf ids, tabs, pos, x, xn, qkv, xq, xqk, sa, qq, sq, kp, ks, vt, vs, ctx, g, pooled, flag;
   DevBuf cmax, gmax;  // row maxima of ctx (per head) and g (per 32 columns)
   DevBuf out_states, out_pooled, out_zp, out_zt;  // host-path staging of a pass's outputs
   PinBuf host, flag_host;
@@ -369,6 +369,10 @@ int set_tuning(Tuning &t, int option, int64_t v, bool model_opts) {
     if (v != 0 && v != 1) return bad();
     t.fuse_mlp = (int)v;
     return IXH_OK;
+  case IXH_OPT_QKV_KBLOCK:
+    if (v != 0 && v != 1) return bad();
+    t.qkv_kblock = (int)v;
+    return IXH_OK;
   default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
   }
 }
@@ -384,6 +388,7 @@ int get_tuning(const Tuning &t, int option, int64_t *v) {
   case IXH_OPT_LN_SEG: *v = t.ln_seg; return IXH_OK;
   case IXH_OPT_FUSE_RES: *v = t.fuse_res; return IXH_OK;
   case IXH_OPT_FUSE_MLP: *v = t.fuse_mlp; return IXH_OK;
+  case IXH_OPT_QKV_KBLOCK: *v = t.qkv_kblock; return IXH_OK;
   default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
   }
 }
@@ -661,12 +666,18 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   const bool fuse_mlp = fuse_res && tune.fuse_mlp != 0 &&
                         mlp_res_supported(H, I, KpH, KpI, m->layers[0].i.np) && m->layers[0].i.qk.p &&
                         m->layers[0].omlp.qk.p && gelu_fma_cols(I, c.lanes) == I;
+  // the fused QKV kernel's input rows K-blocked (the weight rows then stay
+  // in LDS): written by a re-layout after the embedding LayerNorm and by
+  // the MLP kernel of each layer
+  const bool kblock = fused && fuse_mlp && tune.qkv_kblock != 0 && qkv_kblock_supported(KpH) &&
+                      m->layers[0].qkv.qk.p;
 
   int rc;
   const size_t ntab = 2 * (size_t)(B + 1) + blocks.size() + B;
   if ((rc = w->tabs.ensure(4 * ntab)) || (rc = w->pos.ensure(4 * (size_t)N)) ||
       (rc = w->x.ensure(4 * (size_t)N * H)) || (rc = w->xn.ensure(4 * (size_t)N * H)) ||
       (!fused && (rc = w->qkv.ensure(4 * (size_t)N * 3 * H))) || (rc = w->xq.ensure((size_t)N * ldq)) ||
+      (kblock && (rc = w->xqk.ensure((size_t)N * KpH))) ||
       (rc = w->sa.ensure(4 * (size_t)N)) || (rc = w->qq.ensure((size_t)N * H)) ||
       (rc = w->sq.ensure(4 * (size_t)N * nh)) || (rc = w->kp.ensure((size_t)nh * Npad * D)) ||
       (rc = w->ks.ensure(4 * (size_t)nh * Npad)) || (rc = w->vt.ensure((size_t)nh * D * Npad)) ||
@@ -751,6 +762,8 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   ra.sa = w->sa.as<float>();
   ra.seg = tune.ln_seg;
   RUN("emb_ln_quant", 0, dN * (4 + row_bytes + 4 * dH + dH + 4), launch_rownorm(ra, st));
+  if (kblock)
+    RUN("kblock", 0, 2 * dN * KpH, launch_kblock_rows(w->xq.as<int8_t>(), KpH, N, KpH, w->xqk.as<int8_t>(), st));
 
   auto gemm = [&](int epi, const Mat &M, int Kp, float *C, int ldc, int n_valid) {
     GemmArgs g{};
@@ -869,6 +882,10 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
     g.qq = w->qq.as<int8_t>();
     g.sq = w->sq.as<float>();
     g.attn_scale = aa.scale;
+    if (kblock) {
+      g.Ak = w->xqk.as<int8_t>();
+      g.ak_rows = N;
+    }
     // attention (infer.go:437-518)
     aa.window = global ? -1 : c.local_attention / 2;
     if (fused) {
@@ -942,6 +959,10 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
       ma.Q = w->xq.as<int8_t>();
       ma.ldq = KpH;
       ma.SA = w->sa.as<float>();
+      if (kblock && next) {
+        ma.Qk = w->xqk.as<int8_t>();
+        ma.qk_rows = N;
+      }
       RUN("mlp_ln", 2 * dN * 2 * dI * dH + 2 * dN * dH * dI,
           dN * (dH + 4) + 3 * dI * dH + 12 * (2 * dI + dH) + dN * 8 * dH + (next ? dN * (dH + 4) : 0),
           launch_mlp_res(ma, c.lanes, st));

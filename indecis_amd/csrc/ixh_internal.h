@@ -26,6 +26,7 @@ struct Tuning {
   int ln_seg = 1;         // LayerNorm lanes 8/16: 1 segment kernel, 0 whole-row LDS kernel
   int fuse_res = 1;       // residual GEMMs fused with quantizeA of their input and the next LN
   int fuse_mlp = 1;       // the MLP block (Wi, GeGLU, quantizeA, WoMLP, next LN) as one kernel
+  int qkv_kblock = 1;     // the fused QKV kernel reads its input rows K-blocked (1) or row-major (0)
 };
 
 // Compute units of the current device (cached per device; 256 if the query
@@ -78,6 +79,10 @@ struct GemmArgs {
   // for c < rmax_ld (the row maxima the fused residual GEMM quantises by)
   float *rmax = nullptr;
   int rmax_ld = 0;
+  // fused QKV kernel: when not null, A K-blocked as [Kp/32][ak_rows][32]
+  // (32 bytes of a row per K-block, a sequence's rows contiguous)
+  const int8_t *Ak = nullptr;
+  int ak_rows = 0;
 };
 
 void launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
@@ -116,6 +121,10 @@ struct ResArgs {
   int8_t *Q;             // [M][ldq] quantised LayerNorm output
   int ldq;
   float *SA;             // [M] its scales
+  // when not null, Q is written K-blocked here instead ([H/32][qk_rows][32],
+  // the fused QKV kernel's K-blocked input)
+  int8_t *Qk = nullptr;
+  int qk_rows = 0;
 };
 bool gemm_res_supported(int H, int Kp, int Np);
 bool launch_gemm_res(const ResArgs &a, int lanes, hipStream_t s);
@@ -146,6 +155,10 @@ struct MlpArgs {
   int8_t *Q;             // [M][ldq] quantised LayerNorm output
   int ldq;
   float *SA;             // [M] its scales
+  // when not null, Q is written K-blocked here instead ([H/32][qk_rows][32],
+  // the fused QKV kernel's K-blocked input)
+  int8_t *Qk = nullptr;
+  int qk_rows = 0;
 };
 bool mlp_res_supported(int H, int I, int KpH, int KpI, int Npi);
 bool launch_mlp_res(const MlpArgs &a, int lanes, hipStream_t s);
@@ -260,5 +273,10 @@ constexpr int kKeyPad = 64;       // key slots of a sequence are padded to this
 // (2 only for an even head count where the device grants the LDS).
 constexpr int kQkvSeqMax = 512;
 void launch_qkv_attn(const GemmArgs &g, const AttnArgs &a, const int32_t *order, int heads, hipStream_t s);
+// The fused QKV kernel's K-blocked input: supported for Kp (a multiple of
+// 128, the weight rows resident in LDS), and the re-layout of row-major
+// int8 rows [M][ldq] (Kp bytes used) into [Kp/32][M][32].
+bool qkv_kblock_supported(int Kp);
+void launch_kblock_rows(const int8_t *q, int ldq, int M, int Kp, int8_t *qk, hipStream_t s);
 
 }  // namespace ixh

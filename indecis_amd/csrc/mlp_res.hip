@@ -476,6 +476,16 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
   }
   lds_barrier();
   constexpr int C16 = H / 16;  // 16-byte pieces of a row
+  if (a.Qk) {
+    // K-blocked: 32-byte block kb of row r at (kb * qk_rows + m0 + r) * 32;
+    // consecutive threads take consecutive rows of one block
+    for (int idx = tid; idx < BM * C16; idx += 512) {
+      const int kb = idx / (2 * BM), rem = idx - kb * 2 * BM, row = rem >> 1, p = rem & 1;
+      if (row < rows)
+        *(v4i *)(a.Qk + ((size_t)kb * a.qk_rows + m0 + row) * 32 + 16 * p) = *(const v4i *)(qs + row * H + 32 * kb + 16 * p);
+    }
+    return;
+  }
   for (int idx = tid; idx < BM * C16; idx += 512) {
     const int row = idx / C16, c = idx - row * C16;
     if (row < rows) *(v4i *)(a.Q + (size_t)(m0 + row) * a.ldq + 16 * c) = *(const v4i *)(qs + row * H + 16 * c);

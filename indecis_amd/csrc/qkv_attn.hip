@@ -28,6 +28,14 @@
 // sequence's rows are read 18 times instead of 36. Workgroups are dealt so
 // that those of a sequence (12 heads x Q, K, V) run on one XCD and share
 // its rows in L2; sequences go longest first, spread over the 8 XCDs.
+//
+// K-blocked input (GemmArgs::Ak, one head, KB): the rows come K-blocked,
+// [Kp/32][rows][32], so a wave's A fragment (32 rows x 32 bytes) is 1 KB
+// contiguous in HBM. The head's weight rows then stay in LDS for the whole
+// K loop (64 rows x Kp bytes, K-blocked from the weights' K-blocked copy),
+// and each wave streams its own row blocks' fragments into registers, PF
+// K-blocks ahead: no ring, no barrier in the K loop, LDS read traffic of B
+// only.
 #include "ixh_device.h"
 #include "ixh_internal.h"
 
@@ -61,8 +69,9 @@ __device__ __forceinline__ void wait_vmcnt_upto(int n) {
   else wait_vmcnt<3>();
 }
 
-template <int NH>
+template <int NH, bool KB>
 __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnArgs a, const int32_t *order) {
+  static_assert(!KB || NH == 1, "K-blocked input: one head a workgroup");
   using S = Shape<NH>;
   constexpr int NW = S::NW, RING = S::RING, STAGE = S::STAGE;
   extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
@@ -152,6 +161,52 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
+  if constexpr (KB) {
+    // the head's weight rows, resident: K-block kb's column tile j as 1 KB
+    // at smem + 1024 (2 kb + j), lane l of a fragment at 16 l (row l % 32,
+    // bytes 16 (l / 32) of the block), loaded as such by chunk q = 2 kb + j
+    const int nkb = g.Kp / 32;
+    for (int q = wave_u; q < 2 * nkb; q += NW) {
+      const int8_t *src = g.Bk + ((size_t)(q >> 1) * g.Np + colb + 32 * (q & 1) + fr) * 32 + 16 * fh;
+      __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(smem + 1024 * q), 16, 0, 0);
+    }
+    // this lane's A rows in K-block 0 (rows past n: row n-1, never
+    // stored), a K-block further on every ak_rows rows
+    constexpr int PF = 2;  // K-blocks in flight (3 spills: 128 VGPRs at four waves a SIMD)
+    const int8_t *arow[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      arow[i] = g.Ak + (size_t)(base + min(32 * (wv_u + 8 * i) + fr, n - 1)) * 32 + 16 * fh;
+    const size_t akstep = (size_t)g.ak_rows * 32;
+    const bool two = wv_u + 8 < nbc;  // this wave's second row block
+    v4i fa[PF][2];
+    auto loadA = [&](int kb, v4i *dst) {
+      dst[0] = *(const v4i *)(arow[0] + kb * akstep);
+      if (two) dst[1] = *(const v4i *)(arow[1] + kb * akstep);
+    };
+#pragma unroll
+    for (int u = 0; u < PF; u++) loadA(u, fa[u]);
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();  // every wave's weight chunks are in LDS
+    if (wv_u < nbc) {
+      for (int k0 = 0; k0 < nkb; k0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; u++) {
+          const int kb = k0 + u;
+          v4i fb[2];
+#pragma unroll
+          for (int j = 0; j < 2; j++) fb[j] = *(const v4i *)(smem + 1024 * (2 * kb + j) + 16 * lane);
+#pragma unroll
+          for (int j = 0; j < 2; j++) acc[0][j] = mfma32(fa[u][0], fb[j], acc[0][j]);
+          if (two) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[1][j] = mfma32(fa[u][1], fb[j], acc[1][j]);
+          }
+          if (kb + PF < nkb) loadA(kb + PF, fa[u]);
+        }
+      }
+    }
+  } else {
   const int nk = g.Kp / BK;
   issue(0);
   if (RING > 2 && nk > 1) issue(1);
@@ -183,6 +238,7 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
       }
     }
   }
+  }  // !KB
   if (tid < 32 * nb) sa_s[tid] = sa_v;
   __syncthreads();  // the ring is no longer read; the row scales are in LDS
 
@@ -315,20 +371,20 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
         PUT(t)
         __syncthreads();
         if (wv == 0) {
-          // the sums stay in key order; KB slab reads are issued together
-          // before their KB adds, so the chain waits on LDS once a batch
-          // (KB = 8 where NH = 2 leaves fewer registers)
-          constexpr int KB = NH == 1 ? 16 : 8;
+          // the sums stay in key order; KN slab reads are issued together
+          // before their KN adds, so the chain waits on LDS once a batch
+          // (KN = 8 where NH = 2 leaves fewer registers)
+          constexpr int KN = NH == 1 ? 16 : 8;
           const int cnt = min(256, n - 256 * t);
           const float *col = slab + lane;
           int lr = 0;
-          for (; lr + KB <= cnt; lr += KB) {
-            float bt[KB];
+          for (; lr + KN <= cnt; lr += KN) {
+            float bt[KN];
 #pragma unroll
-            for (int u = 0; u < KB; u++) bt[u] = col[(lr + u) * KT_LD];
+            for (int u = 0; u < KN; u++) bt[u] = col[(lr + u) * KT_LD];
             __builtin_amdgcn_sched_barrier(0);  // every read issued before the first add
 #pragma unroll
-            for (int u = 0; u < KB; u++) ksum = ksum + bt[u];
+            for (int u = 0; u < KN; u++) ksum = ksum + bt[u];
           }
           for (; lr < cnt; lr++) ksum = ksum + col[lr * KT_LD];
         }
@@ -427,24 +483,44 @@ namespace {
 
 // hipFuncSetAttribute once per variant: 1 set, -1 refused (that variant is
 // then not used), 0 not tried yet.
-template <int NH>
+template <int NH, bool KB>
 bool smem_ready() {
   static int state = 0;
   if (state == 0)
-    state = hipFuncSetAttribute((const void *)qkv_attn_kernel<NH>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    state = hipFuncSetAttribute((const void *)qkv_attn_kernel<NH, KB>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 Shape<NH>::SMEM) == hipSuccess
                 ? 1
                 : -1;
   return state > 0;
 }
 
-template <int NH>
+template <int NH, bool KB>
 void launch_nh(const GemmArgs &g, const AttnArgs &a, const int32_t *order, hipStream_t s) {
   const int grid = NXCD * 3 * (a.nh / NH) * ((a.B + NXCD - 1) / NXCD);
-  qkv_attn_kernel<NH><<<grid, 512 * NH, Shape<NH>::SMEM, s>>>(g, a, order);
+  qkv_attn_kernel<NH, KB><<<grid, 512 * NH, Shape<NH>::SMEM, s>>>(g, a, order);
+}
+
+// Row-major rows to the K-blocked layout [Kp/32][M][32]: thread t moves
+// 16-byte piece t % 2 of row (t / 2) % M of K-block t / (2 M), so a wave's
+// stores are 1 KB contiguous.
+__global__ __launch_bounds__(256) void kblock_rows_kernel(const int8_t *q, int ldq, int M, int nkb, int8_t *qk) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= 2LL * M * nkb) return;
+  const int piece = (int)(t & 1);
+  const long long rk = t >> 1;
+  const int row = (int)(rk % M), kb = (int)(rk / M);
+  *(v4i *)(qk + ((size_t)kb * M + row) * 32 + 16 * piece) = *(const v4i *)(q + (size_t)row * ldq + 32 * kb + 16 * piece);
 }
 
 }  // namespace
+
+bool qkv_kblock_supported(int Kp) { return Kp % 128 == 0 && Kp * 64 <= Shape<1>::SMEM; }
+
+void launch_kblock_rows(const int8_t *q, int ldq, int M, int Kp, int8_t *qk, hipStream_t s) {
+  if (M <= 0) return;
+  const long long n = 2LL * M * (Kp / 32);
+  kblock_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(q, ldq, M, Kp / 32, qk);
+}
 
 // One head a workgroup; two (1,024 threads) on request when the
 // head count is even and the device grants the LDS. Two heads halve the
@@ -454,12 +530,15 @@ void launch_nh(const GemmArgs &g, const AttnArgs &a, const int32_t *order, hipSt
 // 315 us a launch).
 void launch_qkv_attn(const GemmArgs &g, const AttnArgs &a, const int32_t *order, int heads, hipStream_t s) {
   if (a.B <= 0) return;
-  const bool pair = heads == 2 && a.nh % 2 == 0;
-  if (pair && smem_ready<2>()) {
-    launch_nh<2>(g, a, order, s);
+  const bool pair = heads == 2 && a.nh % 2 == 0 && !g.Ak;
+  if (pair && smem_ready<2, false>()) {
+    launch_nh<2, false>(g, a, order, s);
+  } else if (g.Ak) {
+    (void)smem_ready<1, true>();
+    launch_nh<1, true>(g, a, order, s);
   } else {
-    (void)smem_ready<1>();
-    launch_nh<1>(g, a, order, s);
+    (void)smem_ready<1, false>();
+    launch_nh<1, false>(g, a, order, s);
   }
 }
 
