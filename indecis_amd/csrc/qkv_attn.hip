@@ -244,41 +244,51 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
 
   // ---- dequantisation (and RoPE on Q and K) in the MFMA layout ----
   // lane: columns fr and 32 + fr of the head, rows 32 rb + acc_row(r)
+  // RoPE tables (cos, sin: 32 floats a position; a row's position is its
+  // index in the sequence, padding rows n-1) of a block's 32 rows, staged
+  // into this wave's 8 KB of the free ring by 8 direct-to-LDS loads: the
+  // first block's issued before the dequantisation of both blocks, the
+  // second's once the first block's are read
   float v[2][2][16];
+  const bool rope = part < 2;
+  const float *tab = (const float *)(smem + wave * 8192);
+  auto tables = [&](int i) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int p = min(32 * (wv + 8 * i) + 8 * u + (lane >> 3), n - 1);
+      const size_t off = (size_t)p * 32 + 4 * (lane & 7);
+      __builtin_amdgcn_global_load_lds((glb_ptr)(g.rope_cos + off), (lds_ptr)(smem + wave * 8192 + 1024 * u), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((glb_ptr)(g.rope_sin + off), (lds_ptr)(smem + wave * 8192 + 4096 + 1024 * u), 16, 0, 0);
+    }
+  };
+  if (rope && wv < nb) tables(0);
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     if (wv + 8 * i >= nb) continue;
-    // RoPE tables (cos, sin: 32 floats a position) of the block's 32 rows,
-    // staged into this wave's 8 KB of the free ring by 8 direct-to-LDS
-    // loads; a row's position is its index in the sequence (padding rows:
-    // n-1)
-    const float *tab = (const float *)(smem + wave * 8192);
-    if (part < 2) {
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const int p = min(32 * (wv + 8 * i) + 8 * u + (lane >> 3), n - 1);
-        const size_t off = (size_t)p * 32 + 4 * (lane & 7);
-        __builtin_amdgcn_global_load_lds((glb_ptr)(g.rope_cos + off), (lds_ptr)(smem + wave * 8192 + 1024 * u), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((glb_ptr)(g.rope_sin + off),
-                                         (lds_ptr)(smem + wave * 8192 + 4096 + 1024 * u), 16, 0, 0);
-      }
-      wait_vmcnt<0>();
-    }
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const int row = 32 * (wv + 8 * i) + acc_row(r, lane);
-      const float sa = sa_s[row];
-      float v0 = deq(acc[i][0][r] + c128[0], zc[0], sb[0], sa);
-      float v1 = deq(acc[i][1][r] + c128[1], zc[1], sb[1], sa);
-      if (part < 2) {
+      const float sa = sa_s[32 * (wv + 8 * i) + acc_row(r, lane)];
+      v[i][0][r] = deq(acc[i][0][r] + c128[0], zc[0], sb[0], sa);
+      v[i][1][r] = deq(acc[i][1][r] + c128[1], zc[1], sb[1], sa);
+    }
+  }
+  if (rope) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      if (wv + 8 * i >= nb) continue;
+      if (i == 1) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt 0: this wave's reads of the first tables returned
+        tables(1);
+      }
+      wait_vmcnt<0>();
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
         // linalg.Rope (vec_simd.go:408-425): x1' = x1*c - x2*s, x2' = x2*c + x1*s
         const float c = tab[acc_row(r, lane) * 32 + fr], sn = tab[1024 + acc_row(r, lane) * 32 + fr];
-        const float x1 = v0, x2 = v1;
-        v0 = x1 * c - x2 * sn;
-        v1 = x2 * c + x1 * sn;
+        const float x1 = v[i][0][r], x2 = v[i][1][r];
+        v[i][0][r] = x1 * c - x2 * sn;
+        v[i][1][r] = x2 * c + x1 * sn;
       }
-      v[i][0][r] = v0;
-      v[i][1][r] = v1;
     }
   }
   __syncthreads();  // every wave is done with its tables: the ring is free again
