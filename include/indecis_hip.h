@@ -205,9 +205,9 @@ enum {
                               LayerNorm + quantisation as one kernel (needs FUSE_RES != 0);
                               0: Wi and WoMLP as chosen by FUSE_RES */
   IXH_OPT_QKV_KBLOCK = 9,  /* 1 (default): the fused QKV kernel reads its input rows K-blocked
-                              (written by the MLP kernel and a re-layout after the embedding
-                              LayerNorm) and keeps the head's weight rows in LDS (needs
-                              FUSE_MLP); 0: row-major rows through an LDS ring */
+                              (written so by the MLP kernel and the embedding LayerNorm) and
+                              keeps the head's weight rows in LDS (needs FUSE_MLP); 0:
+                              row-major rows through an LDS ring */
 };
 int ixh_model_set_option(ixh_model *m, int option, int64_t value);
 int ixh_model_get_option(ixh_model *m, int option, int64_t *value);

@@ -667,8 +667,8 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
                         mlp_res_supported(H, I, KpH, KpI, m->layers[0].i.np) && m->layers[0].i.qk.p &&
                         m->layers[0].omlp.qk.p && gelu_fma_cols(I, c.lanes) == I;
   // the fused QKV kernel's input rows K-blocked (the weight rows then stay
-  // in LDS): written by a re-layout after the embedding LayerNorm and by
-  // the MLP kernel of each layer
+  // in LDS): written so by the embedding LayerNorm and by the MLP kernel of
+  // each layer
   const bool kblock = fused && fuse_mlp && tune.qkv_kblock != 0 && qkv_kblock_supported(KpH) &&
                       m->layers[0].qkv.qk.p;
 
@@ -760,10 +760,12 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   ra.q = w->xq.as<int8_t>();
   ra.ldq = KpH;
   ra.sa = w->sa.as<float>();
+  if (kblock) {  // layer 0's QKV input, K-blocked (nothing else reads these rows)
+    ra.qk = w->xqk.as<int8_t>();
+    ra.qk_rows = N;
+  }
   ra.seg = tune.ln_seg;
   RUN("emb_ln_quant", 0, dN * (4 + row_bytes + 4 * dH + dH + 4), launch_rownorm(ra, st));
-  if (kblock)
-    RUN("kblock", 0, 2 * dN * KpH, launch_kblock_rows(w->xq.as<int8_t>(), KpH, N, KpH, w->xqk.as<int8_t>(), st));
 
   auto gemm = [&](int epi, const Mat &M, int Kp, float *C, int ldc, int n_valid) {
     GemmArgs g{};

@@ -209,6 +209,10 @@ struct RowArgs {
   int ldq;
   float *sa;               // [M]
   int seg = 1;             // lanes 8/16: segment kernel (1) or whole-row LDS kernel (0)
+  // when not null (with q), the quantised rows go here K-blocked instead,
+  // [H/32][qk_rows][32] (H a multiple of 32; nothing is written to q)
+  int8_t *qk = nullptr;
+  int qk_rows = 0;
 };
 void launch_rownorm(const RowArgs &a, hipStream_t s);
 
@@ -273,10 +277,8 @@ constexpr int kKeyPad = 64;       // key slots of a sequence are padded to this
 // (2 only for an even head count where the device grants the LDS).
 constexpr int kQkvSeqMax = 512;
 void launch_qkv_attn(const GemmArgs &g, const AttnArgs &a, const int32_t *order, int heads, hipStream_t s);
-// The fused QKV kernel's K-blocked input: supported for Kp (a multiple of
-// 128, the weight rows resident in LDS), and the re-layout of row-major
-// int8 rows [M][ldq] (Kp bytes used) into [Kp/32][M][32].
+// The fused QKV kernel's K-blocked input ([Kp/32][rows][32]): supported
+// for Kp a multiple of 128 whose weight rows fit in its LDS.
 bool qkv_kblock_supported(int Kp);
-void launch_kblock_rows(const int8_t *q, int ldq, int M, int Kp, int8_t *qk, hipStream_t s);
 
 }  // namespace ixh

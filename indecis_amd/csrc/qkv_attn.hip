@@ -510,27 +510,9 @@ void launch_nh(const GemmArgs &g, const AttnArgs &a, const int32_t *order, hipSt
   qkv_attn_kernel<NH, KB><<<grid, 512 * NH, Shape<NH>::SMEM, s>>>(g, a, order);
 }
 
-// Row-major rows to the K-blocked layout [Kp/32][M][32]: thread t moves
-// 16-byte piece t % 2 of row (t / 2) % M of K-block t / (2 M), so a wave's
-// stores are 1 KB contiguous.
-__global__ __launch_bounds__(256) void kblock_rows_kernel(const int8_t *q, int ldq, int M, int nkb, int8_t *qk) {
-  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (t >= 2LL * M * nkb) return;
-  const int piece = (int)(t & 1);
-  const long long rk = t >> 1;
-  const int row = (int)(rk % M), kb = (int)(rk / M);
-  *(v4i *)(qk + ((size_t)kb * M + row) * 32 + 16 * piece) = *(const v4i *)(q + (size_t)row * ldq + 32 * kb + 16 * piece);
-}
-
 }  // namespace
 
 bool qkv_kblock_supported(int Kp) { return Kp % 128 == 0 && Kp * 64 <= Shape<1>::SMEM; }
-
-void launch_kblock_rows(const int8_t *q, int ldq, int M, int Kp, int8_t *qk, hipStream_t s) {
-  if (M <= 0) return;
-  const long long n = 2LL * M * (Kp / 32);
-  kblock_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(q, ldq, M, Kp / 32, qk);
-}
 
 // One head a workgroup; two (1,024 threads) on request when the
 // head count is even and the device grants the LDS. Two heads halve the

@@ -18,6 +18,13 @@ namespace ixh {
 
 namespace {
 
+// Byte i of quantised row r: row-major q, or K-blocked qk (32-byte blocks
+// of a row K-blocks apart; a 4-byte piece never straddles a block).
+__device__ __forceinline__ int8_t *qbyte(const RowArgs &a, int r, int i) {
+  return a.qk ? a.qk + ((size_t)(i >> 5) * a.qk_rows + r) * 32 + (i & 31) : a.q + (size_t)r * a.ldq + i;
+}
+
+
 struct RowSrc {
   const RowArgs &a;
   const float *f32;      // row base (f32 input, f32 table or exact row)
@@ -207,16 +214,16 @@ __global__ __launch_bounds__(256) void rownorm_kernel(RowArgs a) {
     s = mx / 127.0f;
     inv = 1.0f / s;
   }
-  int8_t *qrow = a.q + (size_t)r * a.ldq;
   for (int i = first; i < vec_end; i += step) {
     const float4 v = src.load4(i);
     const int q0 = q8(out_at(i, v.x), inv), q1 = q8(out_at(i + 1, v.y), inv);
     const int q2 = q8(out_at(i + 2, v.z), inv), q3 = q8(out_at(i + 3, v.w), inv);
-    *(int *)(qrow + i) = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+    *(int *)qbyte(a, r, i) = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
   }
   if (do_tail) {
-    for (int i = tail_begin; i < H; i++) qrow[i] = (int8_t)q8(out_at(i, src.load1(i)), inv);
-    for (int i = H; i < a.ldq; i++) qrow[i] = 0;
+    for (int i = tail_begin; i < H; i++) *qbyte(a, r, i) = (int8_t)q8(out_at(i, src.load1(i)), inv);
+    if (!a.qk)
+      for (int i = H; i < a.ldq; i++) a.q[(size_t)r * a.ldq + i] = 0;
     a.sa[r] = s;
   }
 }
@@ -320,15 +327,14 @@ __global__ __launch_bounds__(64) void rownorm_seg_kernel(RowArgs a) {
       s = mx[r] / 127.0f;
       inv = 1.0f / s;
     }
-    int8_t *qrow = a.q + (size_t)R * a.ldq;
 #pragma unroll
     for (int c = 0; c < CPL; c++) {
       const float4 v = x[r][c];
       const int q0 = q8(v.x, inv), q1 = q8(v.y, inv), q2 = q8(v.z, inv), q3 = q8(v.w, inv);
-      *(int *)(qrow + 4 * (lane + 64 * c)) =
-          (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+      *(int *)qbyte(a, R, 4 * (lane + 64 * c)) = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
     }
-    for (int i = H + lane; i < a.ldq; i += 64) qrow[i] = 0;
+    if (!a.qk)
+      for (int i = H + lane; i < a.ldq; i += 64) a.q[(size_t)R * a.ldq + i] = 0;
     if (lane == 0) a.sa[R] = s;
   }
 }
@@ -441,15 +447,14 @@ __global__ __launch_bounds__(64) void rownorm_lds_kernel(RowArgs a) {
         s = mx[r] / 127.0f;
         inv = 1.0f / s;
       }
-      int8_t *qrow = a.q + (size_t)R * a.ldq;
 #pragma unroll
       for (int c = 0; c < CPL; c++) {
         const float4 v = *(const float4 *)&xs[r * LD + 4 * (lane + 64 * c)];
         const int q0 = q8(v.x, inv), q1 = q8(v.y, inv), q2 = q8(v.z, inv), q3 = q8(v.w, inv);
-        *(int *)(qrow + 4 * (lane + 64 * c)) =
-            (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
+        *(int *)qbyte(a, R, 4 * (lane + 64 * c)) = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
       }
-      for (int i = H + lane; i < a.ldq; i += 64) qrow[i] = 0;
+      if (!a.qk)
+        for (int i = H + lane; i < a.ldq; i += 64) a.q[(size_t)R * a.ldq + i] = 0;
       if (lane == 0) a.sa[R] = s;
     }
   }

@@ -313,15 +313,16 @@ def test_fused_mlp_block_rows(shape):
 @pytest.mark.parametrize("shape", ["small", "base"])
 def test_qkv_kblock_input_exact(shape):
     """Option qkv_kblock: the fused QKV kernel reading its input rows
-    K-blocked ([K/32][N][32], written by the MLP kernel and by a re-layout
-    after the embedding LayerNorm) with the head's weight rows resident in
-    LDS gives the oracle's bits, in one part and in two."""
+    K-blocked ([K/32][N][32], written so by the MLP kernel and by the
+    embedding LayerNorm) with the head's weight rows resident in LDS gives
+    the oracle's bits, in one part and in two, and so does the row-major
+    ring (qkv_kblock 0)."""
     cfg = small_cfg(layers=3) if shape == "small" else base_cfg(layers=2)
     w, gpu, ora = model_pair(cfg, seed=77, lanes=8)
     rng = np.random.default_rng(77)
     seqs = ids_uniform_lengths(rng, 24, 1, 512, cfg.vocab)
     want, _ = ora.encode_tokens(seqs)
-    for parts in (1, 2):
-        with options(gpu, qkv_kblock=1, parts=parts):
+    for kb, parts in ((1, 1), (1, 2), (0, 1)):
+        with options(gpu, qkv_kblock=kb, parts=parts):
             got = gpu.encode_tokens(seqs)
-        assert f32_bits_equal(got, want), (parts, mismatch_report(got, want))
+        assert f32_bits_equal(got, want), (kb, parts, mismatch_report(got, want))
