@@ -56,14 +56,27 @@ constexpr int BM = 32;  // rows of a workgroup
 constexpr int PF = 2;   // K steps of weight fragments in flight
 constexpr int PA = 12;  // K steps of streamed input in flight (STREAM)
 
+// LDS: the input panel, then the LayerNorm's staged rows: two of the
+// four column quarters at a time where two workgroups a CU still fit
+// (78 KB each), else one
+constexpr int panel_bytes(int KT, bool stream) { return stream ? 3 * BM * 32 : BM * 32 * KT; }
+constexpr int quarters_staged(int KT, int NB, bool stream) {
+  return panel_bytes(KT, stream) + BM * (2 * 32 * NB + 8) * 4 <= 78 * 1024 ? 2 : 1;
+}
+constexpr int smem_bytes(int KT, int NB, bool stream) {
+  return panel_bytes(KT, stream) + BM * (quarters_staged(KT, NB, stream) * 32 * NB + 8) * 4;
+}
+
 template <int KT, int NB, int V, bool LN, bool STREAM>
 __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   constexpr int Kp = 32 * KT;
   constexpr int QC = 32 * NB;     // columns of a wave
   constexpr int H = 4 * QC;
-  constexpr int XLD = QC + 8;     // floats per staged row (conflict-free chains)
+  constexpr int QPS = quarters_staged(KT, NB, STREAM);  // column quarters a stage
+  constexpr int XLD = QPS * QC + 8;  // floats per staged row (conflict-free chains)
   constexpr int CPL = (Kp + 255) / 256;  // float4 a lane per input row
-  constexpr int PANEL = STREAM ? 3 * BM * 32 : BM * Kp;  // ring of 3 K steps, or the whole panel
+  constexpr int PANEL = panel_bytes(KT, STREAM);  // ring of 3 K steps, or the whole panel
+  static_assert(BM * H <= BM * XLD * 4, "the int8 output rows fit over the staged rows");
   extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
   int8_t *const panel = smem;                        // [BM][Kp] or 3 x [BM][32]
   float *const xs = (float *)(smem + PANEL);         // [BM][XLD], then [BM][H] bytes
@@ -245,18 +258,18 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   }
   if constexpr (!LN) return;
 
-  // ---- 4. LayerNorm chains, quarter by quarter ----
+  // ---- 4. LayerNorm chains, QPS quarters at a time ----
   // chains: V > 0: BM*V of them, thread t carrying chains t and t + 256
   // (V 16); chain ch is lane partial ch % V of row ch / V. V 0: one
   // float64 chain a row, threads 0..31.
   constexpr int NCH = V > 0 ? BM * V : BM;
   constexpr int CPT = NCH > 256 ? NCH / 256 : 1;
   auto stage = [&](int q) {
-    if (wave == q) {
+    if (wave >= q && wave < q + QPS) {
 #pragma unroll
       for (int j = 0; j < NB; j++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) xs[acc_row(r, lane) * XLD + 32 * j + fr] = x[j][r];
+        for (int r = 0; r < 16; r++) xs[acc_row(r, lane) * XLD + (wave - q) * QC + 32 * j + fr] = x[j][r];
     }
     __syncthreads();
   };
@@ -264,7 +277,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   double pd = 0.0;
 #pragma unroll
   for (int k = 0; k < CPT; k++) p[k] = 0.f;
-  for (int q = 0; q < 4; q++) {
+  for (int q = 0; q < 4; q += QPS) {
     stage(q);
     if constexpr (V > 0) {
 #pragma unroll
@@ -273,12 +286,12 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
         if (ch < NCH) {
           const float *xr = xs + (ch / V) * XLD + ch % V;
 #pragma unroll
-          for (int e = 0; e < QC / V; e++) p[k] = p[k] + xr[V * e];
+          for (int e = 0; e < QPS * QC / V; e++) p[k] = p[k] + xr[V * e];
         }
       }
     } else if (tid < BM) {
       const float *xr = xs + tid * XLD;
-      for (int e = 0; e < QC; e++) pd += (double)xr[e];
+      for (int e = 0; e < QPS * QC; e++) pd += (double)xr[e];
     }
     __syncthreads();
   }
@@ -296,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
     p[k] = 0.f;
   }
   pd = 0.0;
-  for (int q = 0; q < 4; q++) {
+  for (int q = 0; q < 4; q += QPS) {
     stage(q);
     if constexpr (V > 0) {
 #pragma unroll
@@ -305,7 +318,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
         if (ch < NCH) {
           const float *xr = xs + (ch / V) * XLD + ch % V;
 #pragma unroll
-          for (int e = 0; e < QC / V; e++) {
+          for (int e = 0; e < QPS * QC / V; e++) {
             const float d = xr[V * e] - mean[k];
             p[k] = __builtin_fmaf(d, d, p[k]);
           }
@@ -313,7 +326,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
       }
     } else if (tid < BM) {
       const float *xr = xs + tid * XLD;
-      for (int e = 0; e < QC; e++) {
+      for (int e = 0; e < QPS * QC; e++) {
         const double d = (double)(xr[e] - mean[0]);
         pd += d * d;
       }
@@ -394,7 +407,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
 
 template <int KT, int NB, int V, bool LN, bool STREAM>
 void launch_one(const ResArgs &a, hipStream_t s) {
-  const size_t shm = (size_t)(STREAM ? 3 * BM * 32 : BM * 32 * KT) + (size_t)BM * (32 * NB + 8) * 4;
+  const size_t shm = smem_bytes(KT, NB, STREAM);
   static bool attr = false;
   if (!attr) {
     (void)hipFuncSetAttribute((const void *)gemm_res_kernel<KT, NB, V, LN, STREAM>,
