@@ -592,12 +592,19 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   const float *vsd = a.vs + ((size_t)b * a.nh + h) * D;
   float *orow = a.ctx + (size_t)(base + qi) * H + h * D;
   float mx = 0.f;  // max |ctx| of this (row, head), for the fused Wo GEMM
+  // the V scales of this lane's 32 dimensions, every load issued before
+  // the first store (the compiler cannot tell vs from ctx)
+  float4 vsv[2][4];
+#pragma unroll
+  for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) vsv[dt][g] = *(const float4 *)&vsd[dt * 32 + acc_row(4 * g, lane)];
 #pragma unroll
   for (int dt = 0; dt < 2; dt++) {
 #pragma unroll
     for (int g = 0; g < 4; g++) {
       const int d0 = dt * 32 + acc_row(4 * g, lane);
-      const float4 v4 = *(const float4 *)&vsd[d0];
+      const float4 v4 = vsv[dt][g];
       const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
       float ov[4];
 #pragma unroll
