@@ -326,3 +326,20 @@ def test_qkv_kblock_input_exact(shape):
         with options(gpu, qkv_kblock=kb, parts=parts):
             got = gpu.encode_tokens(seqs)
         assert f32_bits_equal(got, want), (kb, parts, mismatch_report(got, want))
+
+
+@pytest.mark.parametrize("lanes", [8, 16])
+def test_ln_whole_row_kernel(lanes):
+    """Option ln_seg 0: the row LayerNorms of lane widths 8 and 16 (the
+    embedding one, which also writes the QKV input K-blocked, and the final
+    one) on the whole-row LDS kernel instead of the segment kernel give the
+    oracle's bits, with the K-blocked QKV input and without it."""
+    cfg = small_cfg(layers=2)
+    w, gpu, ora = model_pair(cfg, seed=9, lanes=lanes)
+    rng = np.random.default_rng(90 + lanes)
+    seqs = ids_uniform_lengths(rng, 6, 1, 300, cfg.vocab)
+    want, _ = ora.encode_tokens(seqs)
+    for kb in (1, 0):
+        with options(gpu, ln_seg=0, qkv_kblock=kb):
+            got = gpu.encode_tokens(seqs)
+        assert f32_bits_equal(got, want), (kb, mismatch_report(got, want))
