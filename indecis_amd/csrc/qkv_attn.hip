@@ -172,17 +172,23 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
     }
     // this lane's A rows in K-block 0 (rows past n: row n-1, never
     // stored), a K-block further on every ak_rows rows
-    constexpr int PF = 2;  // K-blocks in flight (3 spills: 128 VGPRs at four waves a SIMD)
+    constexpr int PF = 4;  // K-blocks in flight (nkb is a multiple of 4)
     const int8_t *arow[2];
 #pragma unroll
     for (int i = 0; i < 2; i++)
       arow[i] = g.Ak + (size_t)(base + min(32 * (wv_u + 8 * i) + fr, n - 1)) * 32 + 16 * fh;
     const size_t akstep = (size_t)g.ak_rows * 32;
     const bool two = wv_u + 8 < nbc;  // this wave's second row block
+    // Both row blocks' fragments are loaded every K-block, past the last
+    // K-block the last one again, whether or not the wave has a second
+    // block (then row n-1: one 32-byte piece): with a load count that does
+    // not depend on the wave or the step, the compiler waits for exactly
+    // the fragment it needs, not for every load in flight.
     v4i fa[PF][2];
     auto loadA = [&](int kb, v4i *dst) {
+      kb = min(kb, nkb - 1);
       dst[0] = *(const v4i *)(arow[0] + kb * akstep);
-      if (two) dst[1] = *(const v4i *)(arow[1] + kb * akstep);
+      dst[1] = *(const v4i *)(arow[1] + kb * akstep);
     };
 #pragma unroll
     for (int u = 0; u < PF; u++) loadA(u, fa[u]);
@@ -202,7 +208,7 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
 #pragma unroll
             for (int j = 0; j < 2; j++) acc[1][j] = mfma32(fa[u][1], fb[j], acc[1][j]);
           }
-          if (kb + PF < nkb) loadA(kb + PF, fa[u]);
+          loadA(kb + PF, fa[u]);
         }
       }
     }
