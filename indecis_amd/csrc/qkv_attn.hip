@@ -36,6 +36,8 @@
 // and each wave streams its own row blocks' fragments into registers, PF
 // K-blocks ahead: no ring, no barrier in the K loop, LDS read traffic of B
 // only.
+#include <type_traits>
+
 #include "ixh_device.h"
 #include "ixh_internal.h"
 
@@ -153,13 +155,17 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
         __builtin_amdgcn_global_load_lds((glb_ptr)(csrc[c] + kt * BK), (lds_ptr)(st + cdst[c]), 16, 0, 0);
   };
 
+  // (the K-blocked loop starts its sums from the MFMAs' zero operand and
+  // zeroes only the blocks stored but not computed)
   v16i acc[2][2];
+  if constexpr (!KB) {
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+  }
 
   if constexpr (KB) {
     // the head's weight rows, resident: K-block kb's column tile j as 1 KB
@@ -171,13 +177,15 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
       __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(smem + 1024 * q), 16, 0, 0);
     }
     // this lane's A rows in K-block 0 (rows past n: row n-1, never
-    // stored), a K-block further on every ak_rows rows
+    // stored), a K-block further on every ak_rows rows: the lane's byte
+    // offsets in the VGPRs, the K-block's in an SGPR (no address
+    // arithmetic a load)
     constexpr int PF = 4;  // K-blocks in flight (nkb is a multiple of 4)
-    const int8_t *arow[2];
+    const auto ars = buf_rsrc(g.Ak, (uint32_t)nkb * g.ak_rows * 32);
+    uint32_t avo[2];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-      arow[i] = g.Ak + (size_t)(base + min(32 * (wv_u + 8 * i) + fr, n - 1)) * 32 + 16 * fh;
-    const size_t akstep = (size_t)g.ak_rows * 32;
+    for (int i = 0; i < 2; i++) avo[i] = (uint32_t)(base + min(32 * (wv_u + 8 * i) + fr, n - 1)) * 32 + 16 * fh;
+    const uint32_t akstep = (uint32_t)g.ak_rows * 32;
     const bool two = wv_u + 8 < nbc;  // this wave's second row block
     // Both row blocks' fragments are loaded every K-block, past the last
     // K-block the last one again, whether or not the wave has a second
@@ -186,32 +194,44 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
     // the fragment it needs, not for every load in flight.
     v4i fa[PF][2];
     auto loadA = [&](int kb, v4i *dst) {
-      kb = min(kb, nkb - 1);
-      dst[0] = *(const v4i *)(arow[0] + kb * akstep);
-      dst[1] = *(const v4i *)(arow[1] + kb * akstep);
+      const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)min(kb, nkb - 1) * akstep);
+      dst[0] = __builtin_amdgcn_raw_buffer_load_b128(ars, avo[0], so, 0);
+      dst[1] = __builtin_amdgcn_raw_buffer_load_b128(ars, avo[1], so, 0);
     };
 #pragma unroll
     for (int u = 0; u < PF; u++) loadA(u, fa[u]);
     wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();  // every wave's weight chunks are in LDS
-    if (wv_u < nbc) {
-      for (int k0 = 0; k0 < nkb; k0 += PF) {
+    // PF K-blocks from k0; the first round's first K-block starts the sums
+    auto round = [&](int k0, auto first) {
 #pragma unroll
-        for (int u = 0; u < PF; u++) {
-          const int kb = k0 + u;
-          v4i fb[2];
+      for (int u = 0; u < PF; u++) {
+        const int kb = k0 + u;
+        const bool z = decltype(first)::value && u == 0;
+        v4i fb[2];
 #pragma unroll
-          for (int j = 0; j < 2; j++) fb[j] = *(const v4i *)(smem + 1024 * (2 * kb + j) + 16 * lane);
+        for (int j = 0; j < 2; j++) fb[j] = *(const v4i *)(smem + 1024 * (2 * kb + j) + 16 * lane);
 #pragma unroll
-          for (int j = 0; j < 2; j++) acc[0][j] = mfma32(fa[u][0], fb[j], acc[0][j]);
-          if (two) {
+        for (int j = 0; j < 2; j++) acc[0][j] = mfma32(fa[u][0], fb[j], z ? v16i{} : acc[0][j]);
+        if (two) {
 #pragma unroll
-            for (int j = 0; j < 2; j++) acc[1][j] = mfma32(fa[u][1], fb[j], acc[1][j]);
-          }
-          loadA(kb + PF, fa[u]);
+          for (int j = 0; j < 2; j++) acc[1][j] = mfma32(fa[u][1], fb[j], z ? v16i{} : acc[1][j]);
         }
+        loadA(kb + PF, fa[u]);
       }
+    };
+    if (wv_u < nbc) {
+      round(0, std::true_type{});
+      for (int k0 = PF; k0 < nkb; k0 += PF) round(k0, std::false_type{});
     }
+    // a block past n that is still stored (padding keys): zero sums
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      if (wv_u + 8 * i >= nbc && wv_u + 8 * i < nb)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
   } else {
   const int nk = g.Kp / BK;
   issue(0);
