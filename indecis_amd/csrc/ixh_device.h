@@ -28,6 +28,15 @@ __device__ __forceinline__ int acc_row(int r, int lane) {
 }
 
 __device__ __forceinline__ float fmax32(float a, float b) { return b > a ? b : a; }
+
+// max(m, |v|) for a running maximum of absolute values started at 0 (so m
+// is never NaN): v_max_f32 (IEEE maxNum) returns the operand that is not
+// NaN, which is fmax32(m, |v|) — Go's `if v > m { m = v }` — in one
+// instruction (two of them fuse into v_max3_f32) instead of a compare and
+// a select. For inputs without NaN every order of the maxima gives the
+// same value; NaN inputs are not reproduced lane by lane from the
+// reference's VMAXPS registers (neither are they by the compare form).
+__device__ __forceinline__ float amax(float m, float v) { return __builtin_fmaxf(m, __builtin_fabsf(v)); }
 __device__ __forceinline__ float fmin32(float a, float b) { return b < a ? b : a; }
 
 // roundHalfEven (linalg/int8.go:207-210) == VCVTPS2DQ for |v| < 2^22.

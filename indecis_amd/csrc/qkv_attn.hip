@@ -322,26 +322,27 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
   if (part == 2) {
     // ---- V: max |V| per dimension, scale, quantCols, V^T ----
     float vm[2] = {0.f, 0.f};
+    // every row of a computed block: the rows past n in the last one are
+    // row n-1 again (its A row and row scale), so they leave the maxima as
+    // they are; a block past n that was not computed is left out
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-      if (wv + 8 * i >= nb) continue;
+      if (wv + 8 * i >= nbc) continue;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        if (32 * (wv + 8 * i) + acc_row(r, lane) < n) {
-          vm[0] = fmax32(vm[0], fabsf(v[i][0][r]));
-          vm[1] = fmax32(vm[1], fabsf(v[i][1][r]));
-        }
+        vm[0] = amax(vm[0], v[i][0][r]);
+        vm[1] = amax(vm[1], v[i][1][r]);
       }
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      vm[j] = fmax32(vm[j], __shfl_xor(vm[j], 32));
+      vm[j] = __builtin_fmaxf(vm[j], __shfl_xor(vm[j], 32));
       if (fh == 0) red_s[hf][wv][32 * j + fr] = vm[j];
     }
     __syncthreads();
     if (tidh < D) {
       float vs = 0.f;
-      for (int w = 0; w < 8; w++) vs = fmax32(vs, red_s[hf][w][tidh]);
+      for (int w = 0; w < 8; w++) vs = __builtin_fmaxf(vs, red_s[hf][w][tidh]);
       float vi = 0.f;
       if (vs > 0.f) {  // attention8.go:262-269
         vs = vs / 127.0f;
@@ -457,9 +458,9 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
 #pragma unroll
     for (int c = 0; c < 8; c++) {
       const float4 x = value(c);
-      mx = fmax32(mx, fmax32(fmax32(fabsf(x.x), fabsf(x.y)), fmax32(fabsf(x.z), fabsf(x.w))));
+      mx = amax(amax(amax(amax(mx, x.x), x.y), x.z), x.w);
     }
-    mx = fmax32(mx, __shfl_xor(mx, 16));
+    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
     __asm__ volatile("" ::: "memory");  // keep the second read of the slab
     float sc = 0.f, inv = 0.f;
     if (mx != 0.f) {
