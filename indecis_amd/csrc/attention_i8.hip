@@ -37,7 +37,7 @@ __device__ __forceinline__ float absmax16(const float4 *v) {
   float m = 0.f;
 #pragma unroll
   for (int c = 0; c < 16; c++)
-    m = fmax32(m, fmax32(fmax32(fabsf(v[c].x), fabsf(v[c].y)), fmax32(fabsf(v[c].z), fabsf(v[c].w))));
+    m = amax(amax(amax(amax(m, v[c].x), v[c].y), v[c].z), v[c].w);
   return m;
 }
 
@@ -118,15 +118,15 @@ __global__ __launch_bounds__(256) void attn_long_stats_kernel(AttnArgs a) {
       if (c0 + kStatRows < n) IXH_STAT_LOAD(c0 + kStatRows)
 #pragma unroll
       for (int u = 0; u < 4; u++)
-        vm = make_float4(fmax32(vm.x, fabsf(cur[u].x)), fmax32(vm.y, fabsf(cur[u].y)),
-                         fmax32(vm.z, fabsf(cur[u].z)), fmax32(vm.w, fabsf(cur[u].w)));
+        vm = make_float4(amax(vm.x, cur[u].x), amax(vm.y, cur[u].y),
+                         amax(vm.z, cur[u].z), amax(vm.w, cur[u].w));
     }
     // threads with the same q hold the same 4 dimensions: xor over r0
     for (int t = 4; t < 64; t <<= 1) {
-      vm.x = fmax32(vm.x, __shfl_xor(vm.x, t));
-      vm.y = fmax32(vm.y, __shfl_xor(vm.y, t));
-      vm.z = fmax32(vm.z, __shfl_xor(vm.z, t));
-      vm.w = fmax32(vm.w, __shfl_xor(vm.w, t));
+      vm.x = __builtin_fmaxf(vm.x, __shfl_xor(vm.x, t));
+      vm.y = __builtin_fmaxf(vm.y, __shfl_xor(vm.y, t));
+      vm.z = __builtin_fmaxf(vm.z, __shfl_xor(vm.z, t));
+      vm.w = __builtin_fmaxf(vm.w, __shfl_xor(vm.w, t));
     }
     float4 *red = (float4 *)&kt[0][0][0];  // [wave][q]
     if ((tid & 63) < 4) red[(tid >> 6) * 4 + q] = vm;
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(256) void attn_long_stats_kernel(AttnArgs a) {
     if (tid < 16) {
       const float *rf = (const float *)red;
       float vs = 0.f;
-      for (int w = 0; w < 4; w++) vs = fmax32(vs, rf[w * 16 + tid]);
+      for (int w = 0; w < 4; w++) vs = __builtin_fmaxf(vs, rf[w * 16 + tid]);
       float vi = 0.f;
       if (vs > 0.f) {  // attention8.go:262-269
         vs = vs / 127.0f;
@@ -225,8 +225,8 @@ __global__ __launch_bounds__(512, 4) void attn_prologue_rows_kernel(AttnArgs a) 
         float sc = 0.f;
         if (j < n) {
           const float4 c = make_float4(kr[u].x - mu.x, kr[u].y - mu.y, kr[u].z - mu.z, kr[u].w - mu.w);
-          float mx = fmax32(fmax32(fabsf(c.x), fabsf(c.y)), fmax32(fabsf(c.z), fabsf(c.w)));
-          for (int t = 1; t < 16; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t, 16));
+          float mx = amax(amax(amax(amax(0.f, c.x), c.y), c.z), c.w);
+          for (int t = 1; t < 16; t <<= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, t, 16));
           float inv = 0.f;
           if (mx != 0.f) {
             sc = mx / 127.0f;
@@ -253,19 +253,19 @@ __global__ __launch_bounds__(512, 4) void attn_prologue_rows_kernel(AttnArgs a) 
       float4 vm = zero4;
 #pragma unroll
       for (int u = 0; u < 16; u++)
-        vm = make_float4(fmax32(vm.x, fabsf(vr[u].x)), fmax32(vm.y, fabsf(vr[u].y)),
-                         fmax32(vm.z, fabsf(vr[u].z)), fmax32(vm.w, fabsf(vr[u].w)));
+        vm = make_float4(amax(vm.x, vr[u].x), amax(vm.y, vr[u].y),
+                         amax(vm.z, vr[u].z), amax(vm.w, vr[u].w));
       for (int t = 16; t < 64; t <<= 1) {
-        vm.x = fmax32(vm.x, __shfl_xor(vm.x, t));
-        vm.y = fmax32(vm.y, __shfl_xor(vm.y, t));
-        vm.z = fmax32(vm.z, __shfl_xor(vm.z, t));
-        vm.w = fmax32(vm.w, __shfl_xor(vm.w, t));
+        vm.x = __builtin_fmaxf(vm.x, __shfl_xor(vm.x, t));
+        vm.y = __builtin_fmaxf(vm.y, __shfl_xor(vm.y, t));
+        vm.z = __builtin_fmaxf(vm.z, __shfl_xor(vm.z, t));
+        vm.w = __builtin_fmaxf(vm.w, __shfl_xor(vm.w, t));
       }
       if (lane < 16) *(float4 *)&red[wave][4 * sub] = vm;
       __syncthreads();
       if (tid < D) {
         float vs = 0.f;
-        for (int g = 0; g < 8; g++) vs = fmax32(vs, red[g][tid]);
+        for (int g = 0; g < 8; g++) vs = __builtin_fmaxf(vs, red[g][tid]);
         float vi = 0.f;
         if (vs > 0.f) {  // attention8.go:262-269
           vs = vs / 127.0f;
@@ -304,8 +304,8 @@ __global__ __launch_bounds__(256) void attn_quant_q_kernel(AttnArgs a) {
   if (g >= a.N * a.nh) return;  // whole 16-lane groups leave together
   const int row = g / a.nh, h = g % a.nh;
   const float4 v = *(const float4 *)(a.qkv + (size_t)row * 3 * a.H + h * D + 4 * sub);
-  float mx = fmax32(fmax32(fabsf(v.x), fabsf(v.y)), fmax32(fabsf(v.z), fabsf(v.w)));
-  for (int t = 1; t < 16; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t, 16));
+  float mx = amax(amax(amax(amax(0.f, v.x), v.y), v.z), v.w);
+  for (int t = 1; t < 16; t <<= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, t, 16));
   float s = 0.f, inv = 0.f;
   if (mx != 0.f) {
     s = mx / 127.0f;
@@ -492,7 +492,7 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
       }
     }
   }
-  m = fmax32(m, __shfl_xor(m, 32)) * sqv;
+  m = __builtin_fmaxf(m, __shfl_xor(m, 32)) * sqv;
 
   // ---- pass 2: P = RNE(255 exp(s - m)), O^T += V^T . P^T ----
   // P (0..255) enters the MFMA as P - 128 (an int8: the byte P ^ 0x80);
@@ -640,8 +640,8 @@ __global__ __launch_bounds__(256) void check_exp255_kernel(uint32_t lo, uint32_t
     const float p = rne(y);
     const bool decided = fabsf(y - p) <= 0.5f - kExp255Tol;
     const float yv = exp32_simd(v) * 255.0f, ys = exp32_scalar(v) * 255.0f;
-    err_v = fmax32(err_v, fabsf(y - yv));
-    err_s = fmax32(err_s, fabsf(y - ys));
+    err_v = amax(err_v, y - yv);
+    err_s = amax(err_s, y - ys);
     if (decided) {
       bad_v += rne(yv) != p;
       bad_s += rne(ys) != p;
@@ -653,8 +653,8 @@ __global__ __launch_bounds__(256) void check_exp255_kernel(uint32_t lo, uint32_t
     bad_v += __shfl_xor(bad_v, t);
     bad_s += __shfl_xor(bad_s, t);
     amb += __shfl_xor(amb, t);
-    err_v = fmax32(err_v, __shfl_xor(err_v, t));
-    err_s = fmax32(err_s, __shfl_xor(err_s, t));
+    err_v = __builtin_fmaxf(err_v, __shfl_xor(err_v, t));
+    err_s = __builtin_fmaxf(err_s, __shfl_xor(err_s, t));
   }
   if ((threadIdx.x & 63) == 0) {
     atomicAdd(&res[0], bad_v);

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
       float mx = 0.f;
       if (m0 + tid < M) {
         const float *am = a.amax + (size_t)(m0 + tid) * a.P;
-        for (int p = 0; p < a.P; p++) mx = fmax32(mx, am[p]);
+        for (int p = 0; p < a.P; p++) mx = __builtin_fmaxf(mx, am[p]);
       }
       float s = 0.f, inv = 0.f;
       if (mx != 0.f) {  // quantizeA: s = max/127, inv = 1/s (int8.go:175-183)
@@ -156,8 +156,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
       float mx = 0.f;
 #pragma unroll
       for (int c = 0; c < CPL; c++)
-        mx = fmax32(mx, fmax32(fmax32(fabsf(v[u][c].x), fabsf(v[u][c].y)),
-                               fmax32(fabsf(v[u][c].z), fabsf(v[u][c].w))));
+        mx = amax(amax(amax(amax(mx, v[u][c].x), v[u][c].y), v[u][c].z), v[u][c].w);
       mx = wave_max(mx);
       float s = 0.f, inv = 0.f;
       if (mx != 0.f) {  // quantizeA: s = max/127, inv = 1/s (int8.go:175-183)
@@ -365,7 +364,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
       const int row = acc_row(r, lane);
       const float o = ((x[j][r] - mean_s[row]) * rstd_s[row]) * g;
       x[j][r] = o;
-      mx[r] = fmax32(mx[r], fabsf(o));
+      mx[r] = amax(mx[r], o);
     }
   }
   // a half-wave holds one row of each register: its max by DPP (lanes 16-31
@@ -379,7 +378,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   // the row's scale and its inverse, once a row (quantizeA: s = max/127,
   // inv = 1/s, int8.go:175-183)
   if (tid < BM) {
-    const float m = fmax32(fmax32(red_s[0][tid], red_s[1][tid]), fmax32(red_s[2][tid], red_s[3][tid]));
+    const float m = __builtin_fmaxf(__builtin_fmaxf(red_s[0][tid], red_s[1][tid]), __builtin_fmaxf(red_s[2][tid], red_s[3][tid]));
     const float sc = m != 0.f ? m / 127.0f : 0.f;
     inv_s[tid] = m != 0.f ? 1.0f / sc : 0.f;
     if (m0 + tid < M) a.SA[m0 + tid] = sc;

@@ -239,7 +239,7 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
     float mx = 0.f;
 #pragma unroll
     for (int c = 0; c < QV; c++)
-      mx = fmax32(mx, fmax32(fmax32(fabsf(cv[c].x), fabsf(cv[c].y)), fmax32(fabsf(cv[c].z), fabsf(cv[c].w))));
+      mx = amax(amax(amax(amax(mx, cv[c].x), cv[c].y), cv[c].z), cv[c].w);
     mx = row16_max(mx);  // the row's 16 threads are one DPP row
     float s = 0.f, inv = 0.f;
     if (mx != 0.f) {  // quantizeA: s = max/127, inv = 1/s (int8.go:175-183)
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
     float mx = 0.f;
 #pragma unroll
     for (int c = 0; c < QV; c++)
-      mx = fmax32(mx, fmax32(fmax32(fabsf(gv[c].x), fabsf(gv[c].y)), fmax32(fabsf(gv[c].z), fabsf(gv[c].w))));
+      mx = amax(amax(amax(amax(mx, gv[c].x), gv[c].y), gv[c].z), gv[c].w);
     mx = row16_max(mx);  // the row's 16 threads are one DPP row
     float s = 0.f, inv = 0.f;
     if (mx != 0.f) {  // quantizeA: s = max/127, inv = 1/s (int8.go:175-183)
@@ -462,7 +462,7 @@ __global__ __launch_bounds__(512, 1) void mlp_res_kernel(MlpArgs a) {
       o[c].y = ((xv.y - mean) * rstd) * gv.y;
       o[c].z = ((xv.z - mean) * rstd) * gv.z;
       o[c].w = ((xv.w - mean) * rstd) * gv.w;
-      mx = fmax32(mx, fmax32(fmax32(fabsf(o[c].x), fabsf(o[c].y)), fmax32(fabsf(o[c].z), fabsf(o[c].w))));
+      mx = amax(amax(amax(amax(mx, o[c].x), o[c].y), o[c].z), o[c].w);
     }
     mx = row16_max(mx);
     float inv = 0.f;

@@ -198,16 +198,16 @@ __global__ __launch_bounds__(256) void rownorm_kernel(RowArgs a) {
     const float o0 = out_at(i, v.x), o1 = out_at(i + 1, v.y), o2 = out_at(i + 2, v.z),
                 o3 = out_at(i + 3, v.w);
     if (a.out) *(float4 *)(a.out + (size_t)r * H + i) = make_float4(o0, o1, o2, o3);
-    mx = fmax32(mx, fmax32(fmax32(fabsf(o0), fabsf(o1)), fmax32(fabsf(o2), fabsf(o3))));
+    mx = amax(amax(amax(amax(mx, o0), o1), o2), o3);
   }
   if (do_tail)
     for (int i = tail_begin; i < H; i++) {
       const float o = out_at(i, src.load1(i));
       if (a.out) a.out[(size_t)r * H + i] = o;
-      mx = fmax32(mx, fabsf(o));
+      mx = amax(mx, o);
     }
   if (!a.q) return;
-  for (int t = 1; t < TPR; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t, TPR));
+  for (int t = 1; t < TPR; t <<= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, t, TPR));
   // quantizeA (linalg/int8.go:160-191): scale = max/127, inv = 1/scale.
   float s = 0.f, inv = 0.f;
   if (mx != 0.f) {
@@ -478,8 +478,8 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float *x, int
   }
 #pragma unroll
   for (int c = 0; c < CPL; c++)
-    mx = fmax32(mx, fmax32(fmax32(fabsf(v[c].x), fabsf(v[c].y)), fmax32(fabsf(v[c].z), fabsf(v[c].w))));
-  for (int t = 1; t < 64; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t));
+    mx = amax(amax(amax(amax(mx, v[c].x), v[c].y), v[c].z), v[c].w);
+  for (int t = 1; t < 64; t <<= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, t));
   float s = 0.f, inv = 0.f;
   if (mx != 0.f) {
     s = mx / 127.0f;
@@ -508,9 +508,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *x, int ld,
   float mx = 0.f;
   for (int i = 4 * lane; i < K; i += 256) {
     const float4 v = *(const float4 *)(row + i);
-    mx = fmax32(mx, fmax32(fmax32(fabsf(v.x), fabsf(v.y)), fmax32(fabsf(v.z), fabsf(v.w))));
+    mx = amax(amax(amax(amax(mx, v.x), v.y), v.z), v.w);
   }
-  for (int t = 1; t < 64; t <<= 1) mx = fmax32(mx, __shfl_xor(mx, t));
+  for (int t = 1; t < 64; t <<= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, t));
   float s = 0.f, inv = 0.f;
   if (mx != 0.f) {
     s = mx / 127.0f;
