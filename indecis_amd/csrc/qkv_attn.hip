@@ -176,6 +176,7 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
       const int8_t *src = g.Bk + ((size_t)(q >> 1) * g.Np + colb + 32 * (q & 1) + fr) * 32 + 16 * fh;
       __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(smem + 1024 * q), 16, 0, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);  // the A loads below stay younger than these
     // this lane's A rows in K-block 0 (rows past n: row n-1, never
     // stored), a K-block further on every ak_rows rows: the lane's byte
     // offsets in the VGPRs, the K-block's in an SGPR (no address
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
     };
 #pragma unroll
     for (int u = 0; u < PF; u++) loadA(u, fa[u]);
-    wait_vmcnt<0>();
+    wait_vmcnt<2 * PF>();  // this wave's weight chunks (older than its 2 PF A loads)
     __builtin_amdgcn_s_barrier();  // every wave's weight chunks are in LDS
     // PF K-blocks from k0; the first round's first K-block starts the sums
     auto round = [&](int k0, auto first) {
