@@ -155,8 +155,7 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
         __builtin_amdgcn_global_load_lds((glb_ptr)(csrc[c] + kt * BK), (lds_ptr)(st + cdst[c]), 16, 0, 0);
   };
 
-  // (the K-blocked loop starts its sums from the MFMAs' zero operand and
-  // zeroes only the blocks stored but not computed)
+  // (the K-blocked loop starts its sums from the MFMAs' zero operand)
   v16i acc[2][2];
   if constexpr (!KB) {
 #pragma unroll
@@ -225,14 +224,6 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
       round(0, std::true_type{});
       for (int k0 = PF; k0 < nkb; k0 += PF) round(k0, std::false_type{});
     }
-    // a block past n that is still stored (padding keys): zero sums
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-      if (wv_u + 8 * i >= nbc && wv_u + 8 * i < nb)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
   } else {
   const int nk = g.Kp / BK;
   issue(0);
@@ -288,10 +279,12 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
       __builtin_amdgcn_global_load_lds((glb_ptr)(g.rope_sin + off), (lds_ptr)(smem + wave * 8192 + 4096 + 1024 * u), 16, 0, 0);
     }
   };
-  if (rope && wv < nb) tables(0);
+  if (rope && wv < nbc) tables(0);
 #pragma unroll
   for (int i = 0; i < 2; i++) {
-    if (wv + 8 * i >= nb) continue;
+    // a block past n (stored as padding keys) is not computed: its values
+    // reach only rows past n, which every store below writes as zeros
+    if (wv + 8 * i >= nbc) continue;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const float sa = sa_s[32 * (wv + 8 * i) + acc_row(r, lane)];
@@ -302,7 +295,7 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
   if (rope) {
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-      if (wv + 8 * i >= nb) continue;
+      if (wv + 8 * i >= nbc) continue;
       if (i == 1) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt 0: this wave's reads of the first tables returned
         tables(1);
