@@ -350,6 +350,7 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   // (ExpShift's scalar loop over the last len%V values, vec_simd.go:258-262)
   const int cs = global ? 0 : max(0, qi - W);
   const int ce = global ? n : min(n, qi + W + 1);
+  const uint32_t span = (uint32_t)(ce - cs);  // > 0 for an active query
   const int V = a.lanes;
   const int ts = V > 0 ? cs + ((ce - cs) / V) * V : cs;
   // wave-wide bounds over the active queries: a tile [k0, k0+32) with
@@ -484,10 +485,12 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
 #pragma unroll
         for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, sv[r]);  // no NaN: v_max
       } else {
+        // key j valid: cs <= j < ce, as one unsigned compare of j - cs
+        const int jb = k0 - cs + 4 * (lane >> 5);
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const int j = k0 + acc_row(r, lane);
-          m = (j >= cs && j < ce) ? fmax32(m, sv[r]) : m;
+          const bool in = (uint32_t)(jb + 8 * (r >> 2) + (r & 3)) < span;
+          m = __builtin_fmaxf(m, in ? sv[r] : -__builtin_huge_valf());
         }
       }
     }
@@ -561,11 +564,9 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
         }
       }
       if (!full) {
+        const int jb = k0 - cs + 4 * (lane >> 5);
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int j = k0 + acc_row(r, lane);
-          p[r] = (j >= cs && j < ce) ? p[r] : 0.0f;
-        }
+        for (int r = 0; r < 16; r++) p[r] = (uint32_t)(jb + 8 * (r >> 2) + (r & 3)) < span ? p[r] : 0.0f;
       }
       unsigned pw[4];
 #pragma unroll
