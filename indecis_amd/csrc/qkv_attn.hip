@@ -357,15 +357,19 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
         for (int j = 0; j < 2; j++) {
 #pragma unroll
           for (int gq = 0; gq < 4; gq++) {
-            int qv[4];
+            // keys 8gq + 4fh + 0..3 of dimension 32j + fr; keys past n are
+            // zero bytes (a block past n was not computed: all zero)
+            int w = 0;
+            if (rb < nbc) {
+              int qv[4];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-              const int r = 4 * gq + u;
-              qv[u] = 32 * rb + acc_row(r, lane) < n ? q8(v[i][j][r], j ? vi1 : vi0) : 0;
+              for (int u = 0; u < 4; u++) qv[u] = q8(v[i][j][4 * gq + u], j ? vi1 : vi0);
+              const int lim = n - (32 * rb + 8 * gq + 4 * fh);  // keys of the four still in the sequence
+              const unsigned keep = lim >= 4 ? 0xffffffffu : lim <= 0 ? 0u : (1u << (8 * lim)) - 1u;
+              w = (int)(((unsigned)(qv[0] & 0xff) | ((unsigned)(qv[1] & 0xff) << 8) |
+                         ((unsigned)(qv[2] & 0xff) << 16) | ((unsigned)qv[3] << 24)) & keep);
             }
-            // keys 8gq + 4fh + 0..3 of dimension 32j + fr
-            *(int *)(vt_s + (32 * j + fr) * VT_LD + 8 * gq + 4 * fh) =
-                (qv[0] & 0xff) | ((qv[1] & 0xff) << 8) | ((qv[2] & 0xff) << 16) | (qv[3] << 24);
+            *(int *)(vt_s + (32 * j + fr) * VT_LD + 8 * gq + 4 * fh) = w;
           }
         }
       }
