@@ -326,10 +326,12 @@ def test_qkv_kblock_input_exact(shape):
         with options(gpu, qkv_kblock=kb, parts=parts):
             got = gpu.encode_tokens(seqs)
         assert f32_bits_equal(got, want), (kb, parts, mismatch_report(got, want))
-    # the edges of the row blocks (32 rows, one or two a wave: 256) and of
-    # the fused kernel's limit (512 keys)
+    # the edges of the row blocks (32 rows, one or two a wave: 256), of the
+    # K mean's read batches (16 rows, taken two at a time) and of the fused
+    # kernel's limit (512 keys)
     edges = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32)
-             for n in (1, 31, 32, 33, 255, 256, 257, 288, 511, 512)]
+             for n in (1, 15, 16, 17, 31, 32, 33, 47, 48, 49, 255, 256, 257, 271, 272, 273, 288,
+                       303, 511, 512)]
     want, _ = ora.encode_tokens(edges)
     with options(gpu, qkv_kblock=1, parts=1):
         got = gpu.encode_tokens(edges)
