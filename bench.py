@@ -404,6 +404,8 @@ def main():
     ap.add_argument("--inputs", type=int, default=8192, help="inputs (--decide)")
     ap.add_argument("--decide-lo", type=int, default=8)
     ap.add_argument("--decide-hi", type=int, default=256)
+    ap.add_argument("--option", action="append", default=[], metavar="NAME=VALUE",
+                    help="a model option (ixh_model_set_option) for every pass, e.g. fuse_mlp=2")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="instead: the vendor int8 and bf16 GEMMs (torch) on the encoder's GEMM shapes")
     args = ap.parse_args()
@@ -435,6 +437,9 @@ def main():
 
     torch.cuda.set_device(0)
     model = Model(weights, device=0, lanes=args.lanes)
+    for o in args.option:
+        k, v = o.split("=", 1)
+        model.set_option(k, int(v))
     if args.serving:
         serving(np, model, cfg, args)
         model.close()

@@ -201,9 +201,11 @@ enum {
                               streamed in its K loop (attention writes row maxima); 3: also
                               WoMLP's (the GeGLU epilogue writes them); 4: Wo on the
                               whole-row kernel of 8 waves; 0: separate kernels */
-  IXH_OPT_FUSE_MLP = 8,    /* 1 (default): Wi, GeGLU, the quantisation of g, WoMLP and the next
-                              LayerNorm + quantisation as one kernel (needs FUSE_RES != 0);
-                              0: Wi and WoMLP as chosen by FUSE_RES */
+  IXH_OPT_FUSE_MLP = 8,    /* Wi, GeGLU, the quantisation of g, WoMLP and the next LayerNorm +
+                              quantisation as one kernel: 2 (default) 64 rows a workgroup,
+                              transposed products (hidden 768, 384 or 256); 1: 32 rows a
+                              workgroup (hidden 768 or 256, needs FUSE_RES != 0); 0: Wi and
+                              WoMLP as chosen by FUSE_RES */
   IXH_OPT_QKV_KBLOCK = 9,  /* 1 (default): the fused QKV kernel reads its input rows K-blocked
                               (written so by the MLP kernel and the embedding LayerNorm) and
                               keeps the head's weight rows in LDS (needs FUSE_MLP); 0:

@@ -366,7 +366,7 @@ int set_tuning(Tuning &t, int option, int64_t v, bool model_opts) {
     t.fuse_res = (int)v;
     return IXH_OK;
   case IXH_OPT_FUSE_MLP:
-    if (v != 0 && v != 1) return bad();
+    if (v < 0 || v > 2) return bad();
     t.fuse_mlp = (int)v;
     return IXH_OK;
   case IXH_OPT_QKV_KBLOCK:
@@ -661,11 +661,14 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   // fuse_res 4: Wo on the whole-row kernel of 8 waves (mlp_res.hip)
   const bool wo8 = fuse_res && tune.fuse_res == 4 && wo_res_supported(H, KpH, m->layers[0].o.np) &&
                    m->layers[0].o.qk.p;
-  // the whole MLP block as one kernel (mlp_res.hip), where the shapes allow
-  // it; it takes the mlp_norm output quantised by the fused Wo kernel
-  const bool fuse_mlp = fuse_res && tune.fuse_mlp != 0 &&
-                        mlp_res_supported(H, I, KpH, KpI, m->layers[0].i.np) && m->layers[0].i.qk.p &&
-                        m->layers[0].omlp.qk.p && gelu_fma_cols(I, c.lanes) == I;
+  // the whole MLP block as one kernel, where the shapes allow it: 64 rows
+  // a workgroup, transposed (mlp_block.hip; fuse_mlp 2), or 32 rows
+  // (mlp_res.hip; fuse_mlp 1, with the fused Wo kernel). It takes the
+  // quantised mlp_norm output of whichever Wo path ran.
+  const bool mlp_common = m->layers[0].i.qk.p && m->layers[0].omlp.qk.p && gelu_fma_cols(I, c.lanes) == I;
+  const bool mlp_block = mlp_common && tune.fuse_mlp == 2 && mlp_block_supported(H, I, KpH, KpI, m->layers[0].i.np);
+  const bool fuse_mlp = mlp_block || (mlp_common && fuse_res && tune.fuse_mlp != 0 &&
+                                      mlp_res_supported(H, I, KpH, KpI, m->layers[0].i.np));
   // the fused QKV kernel's input rows K-blocked (the weight rows then stay
   // in LDS): written so by the embedding LayerNorm and by the MLP kernel of
   // each layer
@@ -719,6 +722,12 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
     prof.end(pi_, name, (double)(ops), (double)(bytes));                                 \
   } while (0)
 
+  // a fused kernel that refuses its arguments (a shape or option the gates
+  // above let through by mistake) fails the pass instead of leaving x
+  // without its residual and LayerNorm
+  auto refused = [&](const char *k) {
+    return fail(IXH_EINVAL, "indecis: kernel %s refused this model's shapes (H %d, I %d)", k, H, I);
+  };
   // algorithmic figures: valid (query, key) pairs of local and global layers
   double keys_local = 0, keys_global = 0;
   const int Wl = c.local_attention / 2;
@@ -786,6 +795,7 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
     g.n_valid = n_valid;
     g.lanes = c.lanes;
     g.n_gelu = gelu_fma_cols(I, c.lanes);
+    g.tile_cfg = tune.gemm_tile;  // the tiled GEMM's tiles, wherever it runs
     return g;
   };
   // GEMM HBM bytes: activations int8 + scales, weights, output (read too
@@ -923,10 +933,12 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
       wa.Q = w->xq.as<int8_t>();
       wa.ldq = KpH;
       wa.SA = w->sa.as<float>();
-      RUN("gemm_wo_ln", 2 * dN * dH * dH, res_bytes(dH, true), launch_wo_res(wa, c.lanes, st));
+      RUN("gemm_wo_ln", 2 * dN * dH * dH, res_bytes(dH, true),
+          if (!launch_wo_res(wa, c.lanes, st)) return refused("gemm_wo_ln"));
     } else if (fuse_res) {
       const ResArgs r = res(L.o, w->ctx.as<float>(), H, L.mlp_norm.as<float>(), cmax, nh);
-      RUN("gemm_wo_ln", 2 * dN * dH * dH, res_bytes(dH, true), launch_gemm_res(r, c.lanes, st));
+      RUN("gemm_wo_ln", 2 * dN * dH * dH, res_bytes(dH, true),
+          if (!launch_gemm_res(r, c.lanes, st)) return refused("gemm_wo_ln"));
     } else {
       RUN("quant_ctx", 0, dN * (4 * dH + dH + 4),
           launch_quant_rows(w->ctx.as<float>(), H, N, H, w->xq.as<int8_t>(), KpH, w->sa.as<float>(), st));
@@ -949,6 +961,7 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
       ma.c128i = L.i.c128.as<int32_t>();
       ma.n_gelu = gelu_fma_cols(I, c.lanes);
       ma.Bo = L.omlp.qk.as<int8_t>();
+      ma.Npo = L.omlp.np;
       ma.sbo = L.omlp.sb.as<float>();
       ma.zco = L.omlp.zc.as<float>();
       ma.c128o = L.omlp.c128.as<int32_t>();
@@ -967,7 +980,8 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
       }
       RUN("mlp_ln", 2 * dN * 2 * dI * dH + 2 * dN * dH * dI,
           dN * (dH + 4) + 3 * dI * dH + 12 * (2 * dI + dH) + dN * 8 * dH + (next ? dN * (dH + 4) : 0),
-          launch_mlp_res(ma, c.lanes, st));
+          if (!(mlp_block ? launch_mlp_block(ma, c.lanes, st) : launch_mlp_res(ma, c.lanes, st)))
+            return refused("mlp_ln"));
       ln_done = next;
       continue;
     }
@@ -982,7 +996,8 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
       const bool next = l + 1 < c.layers;
       const ResArgs r = res(L.omlp, w->g.as<float>(), I, next ? m->layers[l + 1].attn_norm.as<float>() : nullptr,
                             gmax, I / 32);
-      RUN("gemm_womlp_ln", 2 * dN * dH * dI, res_bytes(dI, next), launch_gemm_res(r, c.lanes, st));
+      RUN("gemm_womlp_ln", 2 * dN * dH * dI, res_bytes(dI, next),
+          if (!launch_gemm_res(r, c.lanes, st)) return refused("gemm_womlp_ln"));
       ln_done = next;
     } else {
       RUN("quant_g", 0, dN * (4 * dI + dI + 4),

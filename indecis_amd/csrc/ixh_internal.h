@@ -25,7 +25,8 @@ struct Tuning {
   int gemm_tile = 0;      // gemm_i8 tiles: 0 128x128/2 stages, 1 256x128/3, 2 128x128/3
   int ln_seg = 1;         // LayerNorm lanes 8/16: 1 segment kernel, 0 whole-row LDS kernel
   int fuse_res = 1;       // residual GEMMs fused with quantizeA of their input and the next LN
-  int fuse_mlp = 1;       // the MLP block (Wi, GeGLU, quantizeA, WoMLP, next LN) as one kernel
+  int fuse_mlp = 2;       // the MLP block (Wi, GeGLU, quantizeA, WoMLP, next LN) as one kernel:
+                          // 2 mlp_block (64 rows, transposed), 1 mlp_res (32 rows), 0 separate
   int qkv_kblock = 1;     // the fused QKV kernel reads its input rows K-blocked (1) or row-major (0)
 };
 
@@ -145,7 +146,8 @@ struct MlpArgs {
   const float *sbi, *zci;  // [Npi]
   const int32_t *c128i;    // [Npi]
   int n_gelu;            // gated columns below it take the FMA-form GELU (must be I)
-  const int8_t *Bo;      // WoMLP K-blocked [I/32][H][32]
+  const int8_t *Bo;      // WoMLP K-blocked [I/32][Npo][32]
+  int Npo = 0;           // its rows a K-block (H padded; 0: H)
   const float *sbo, *zco;  // [H]
   const int32_t *c128o;    // [H]
   float *X;              // [M][H] residual, updated in place
@@ -162,6 +164,12 @@ struct MlpArgs {
 };
 bool mlp_res_supported(int H, int I, int KpH, int KpI, int Npi);
 bool launch_mlp_res(const MlpArgs &a, int lanes, hipStream_t s);
+// The MLP block 64 rows a workgroup with transposed products
+// (mlp_block.hip): same arguments and results as launch_mlp_res; needs
+// (H, I) one of (768, 1152), (384, 1152), (256, 512), unpadded, and
+// n_gelu == I; returns false (nothing launched) otherwise.
+bool mlp_block_supported(int H, int I, int KpH, int KpI, int Npi);
+bool launch_mlp_block(const MlpArgs &a, int lanes, hipStream_t s);
 // The same kernel for Wo (mlp_res.hip, WO mode): X[m] += deq(quantizeA(
 // Af[m][:H]) . Wo^T), then Q/SA = quantizeA(LayerNorm(X[m], gamma)); Bo,
 // sbo, zco, c128o are Wo's (K-blocked [H/32][H][32]). Needs H 768 or 256,

@@ -16,6 +16,13 @@ def base_cfg(**kw):
     return Config(**{**BASE.__dict__, **kw})
 
 
+def bekko_cfg(**kw):
+    """The reference's own int8 backbone width, bekko-embedding-v1-a8m:
+    hidden 384 (6 heads of 64), MLP 2 x 1152 (linalg/gemm_test.go:104-105)."""
+    return Config(**{**BASE.__dict__, "hidden": 384, "heads": 6, "intermediate": 1152,
+                     "vocab": 32768, **kw})
+
+
 def ids_cfg2(rng, B=64, T=15, vocab=32768):
     """cfg2: B x T tokens, ids uniform in [5, vocab), CLS first, SEP last."""
     seqs = []

@@ -8,7 +8,7 @@ import contextlib
 import numpy as np
 import pytest
 
-from helpers import (base_cfg, f32_bits_equal, ids_cfg2, ids_uniform_lengths, mismatch_report,
+from helpers import (base_cfg, bekko_cfg, f32_bits_equal, ids_cfg2, ids_uniform_lengths, mismatch_report,
                      small_cfg)
 from indecis_amd import _lib, heads
 from indecis_amd.modernbert import EMB_BF16, EMB_F32, EMB_I8, Model, Weights
@@ -282,32 +282,74 @@ def test_fused_residual_gemms(shape, lanes):
         seqs.append(rng.integers(0, cfg.vocab, size=5, dtype=np.int32))
     want, _ = ora.encode_tokens(seqs)
     for mode, gemm, mlp in ((1, 0, 1), (1, 0, 0), (2, 0, 0), (3, 0, 0), (0, 0, 0), (3, 1, 0), (2, 0, 1),
-                            (4, 0, 1), (4, 0, 0)):
+                            (4, 0, 1), (4, 0, 0), (1, 0, 2), (0, 0, 2), (4, 0, 2)):
         with options(gpu, fuse_res=mode, gemm=gemm, fuse_mlp=mlp):
             got = gpu.encode_tokens(seqs)
         assert f32_bits_equal(got, want), (mode, gemm, mlp, mismatch_report(got, want))
 
 
-@pytest.mark.parametrize("shape", ["small", "base"])
-def test_fused_mlp_block_rows(shape):
-    """Option fuse_mlp (the default): the MLP block as one kernel (Wi,
-    GeGLU, quantizeA of g, WoMLP, the next LayerNorm + quantizeA;
-    mlp_res.hip), one workgroup per 32 rows, gives the oracle's bits at row
-    counts below, at and around its 32-row blocks, and equals the separate
-    kernels (fuse_mlp 0) on a batch of 4,000 rows."""
-    cfg = small_cfg(layers=2) if shape == "small" else base_cfg(layers=2)
+def _shape_cfg(shape, layers):
+    return {"small": small_cfg, "base": base_cfg, "bekko": bekko_cfg}[shape](layers=layers)
+
+
+@pytest.mark.parametrize("shape,kernel", [("small", 1), ("base", 1), ("small", 2), ("base", 2),
+                                          ("bekko", 2)])
+def test_fused_mlp_block_rows(shape, kernel):
+    """Option fuse_mlp: the MLP block as one kernel (Wi, GeGLU, quantizeA
+    of g, WoMLP, the next LayerNorm + quantizeA), one workgroup per 32 rows
+    (1, mlp_res.hip) or per 64 rows with transposed products (2,
+    mlp_block.hip), gives the oracle's bits at row counts below, at and
+    around its row blocks, and equals the separate kernels (fuse_mlp 0) on
+    a batch of 4,000 rows."""
+    cfg = _shape_cfg(shape, 2)
     w, gpu, ora = model_pair(cfg, seed=73, lanes=8)
     rng = np.random.default_rng(73)
-    for n in (1, 31, 32, 33, 64, 97):
-        seqs = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32)]
-        got = gpu.encode_tokens(seqs)
-        want, _ = ora.encode_tokens(seqs)
-        assert f32_bits_equal(got, want), (n, mismatch_report(got, want))
-    seqs = ids_uniform_lengths(rng, 16, 150, 350, cfg.vocab)
-    fused = gpu.encode_tokens(seqs)
+    with options(gpu, fuse_mlp=kernel):
+        for n in (1, 31, 32, 33, 63, 64, 65, 97, 128, 129):
+            seqs = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32)]
+            got = gpu.encode_tokens(seqs)
+            want, _ = ora.encode_tokens(seqs)
+            assert f32_bits_equal(got, want), (n, mismatch_report(got, want))
+        seqs = ids_uniform_lengths(rng, 16, 150, 350, cfg.vocab)
+        fused = gpu.encode_tokens(seqs)
     with options(gpu, fuse_mlp=0):
         separate = gpu.encode_tokens(seqs)
     assert f32_bits_equal(fused, separate), mismatch_report(fused, separate)
+
+
+@pytest.mark.parametrize("lanes", [0, 4, 8, 16])
+def test_mlp_block_lanes(lanes):
+    """The 64-row MLP kernel (fuse_mlp 2) for every lane width of the
+    LayerNorm chains (float32 lane partials in two column stages at hidden
+    768, or one float64 chain a row), and the last layer without
+    LayerNorm, against the oracle, at both model widths of BASELINE.json."""
+    for shape, layers in (("small", 3), ("base", 2)):
+        cfg = _shape_cfg(shape, layers)
+        w, gpu, ora = model_pair(cfg, seed=79, lanes=lanes)
+        rng = np.random.default_rng(79 + lanes)
+        seqs = ids_uniform_lengths(rng, 9, 1, 300, cfg.vocab)
+        want, _ = ora.encode_tokens(seqs)
+        with options(gpu, fuse_mlp=2):
+            got = gpu.encode_tokens(seqs)
+        assert f32_bits_equal(got, want), (shape, mismatch_report(got, want))
+
+
+def test_bekko_width_exact():
+    """The reference's own backbone width (bekko a8m: hidden 384, 6 heads,
+    MLP 2 x 1152; linalg/gemm_test.go:104-105) through the whole encoder,
+    with the fused kernels on (the 64-row MLP kernel, the fused QKV
+    kernel) and off, pooled and per token, against the oracle."""
+    cfg = bekko_cfg(layers=3)
+    w, gpu, ora = model_pair(cfg, seed=83, lanes=8)
+    rng = np.random.default_rng(83)
+    seqs = ids_uniform_lengths(rng, 12, 1, 400, cfg.vocab)
+    want, _ = ora.encode_tokens(seqs)
+    for mlp, res, qkv in ((2, 1, 1), (0, 0, 0), (2, 0, 0), (1, 1, 1)):
+        with options(gpu, fuse_mlp=mlp, fuse_res=res, qkv_fused=qkv):
+            got = gpu.encode_tokens(seqs)
+            pooled = gpu.encode_seqs(seqs)
+        assert f32_bits_equal(got, want), ((mlp, res, qkv), mismatch_report(got, want))
+        assert f32_bits_equal(pooled, ora.encode_seqs(seqs)), (mlp, res, qkv)
 
 
 @pytest.mark.parametrize("shape", ["small", "base"])
