@@ -124,6 +124,11 @@ struct DeviceGuard {
 struct Mat {
   int k = 0, n = 0, kp = 0, np = 0;
   bool set = false;
+  // every row d has 127 * sum_k |w[d][k]| + |128 * colsum[d]| < 2^24: then
+  // for any int8 activations the reference tile acc + 128*colsum is exact
+  // in float32 and f32(tile) - zc equals f32(acc) (kernels that need it
+  // dequantise as f32(acc) * sb * sa)
+  bool small = false;
   DevBuf q, qk, sb, zc, c128;
 };
 
@@ -152,14 +157,19 @@ int upload_mat(Mat &M, const std::vector<int8_t> &rows, const float *scale, int 
   std::vector<int8_t> q((size_t)M.np * M.kp, 0);
   std::vector<float> sb(M.np, 0.f), zc(M.np, 0.f);
   std::vector<int32_t> c128(M.np, 0);
+  M.small = true;
   for (int d = 0; d < n; d++) {
     const int s = perm ? (*perm)[d] : d;
     int32_t colsum = 0;
+    int64_t l1 = 0;
     for (int t = 0; t < k; t++) {
       const int8_t v = rows[(size_t)s * k + t];
       q[(size_t)d * M.kp + t] = v;
       colsum += v;
+      l1 += v < 0 ? -v : v;
     }
+    // |acc| <= 127 * l1 for activations in [-127, 127]
+    if (127 * l1 + 128 * (int64_t)std::abs(colsum) >= (int64_t)1 << 24) M.small = false;
     sb[d] = scale[s];
     // PackB8: zc = 128*float32(colsum) (int8.go:72-75)
     zc[d] = 128.0f * (float)colsum;
@@ -666,7 +676,10 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   // (mlp_res.hip; fuse_mlp 1, with the fused Wo kernel). It takes the
   // quantised mlp_norm output of whichever Wo path ran.
   const bool mlp_common = m->layers[0].i.qk.p && m->layers[0].omlp.qk.p && gelu_fma_cols(I, c.lanes) == I;
-  const bool mlp_block = mlp_common && tune.fuse_mlp == 2 && mlp_block_supported(H, I, KpH, KpI, m->layers[0].i.np);
+  bool mats_small = true;  // the 64-row kernel dequantises as f32(acc) * sb * sa
+  for (int l = 0; l < c.layers; l++) mats_small = mats_small && m->layers[l].i.small && m->layers[l].omlp.small;
+  const bool mlp_block = mlp_common && tune.fuse_mlp == 2 && mats_small &&
+                         mlp_block_supported(H, I, KpH, KpI, m->layers[0].i.np);
   const bool fuse_mlp = mlp_block || (mlp_common && fuse_res && tune.fuse_mlp != 0 &&
                                       mlp_res_supported(H, I, KpH, KpI, m->layers[0].i.np));
   // the fused QKV kernel's input rows K-blocked (the weight rows then stay

@@ -167,7 +167,10 @@ bool launch_mlp_res(const MlpArgs &a, int lanes, hipStream_t s);
 // The MLP block 64 rows a workgroup with transposed products
 // (mlp_block.hip): same arguments and results as launch_mlp_res; needs
 // (H, I) one of (768, 1152), (384, 1152), (256, 512), unpadded, and
-// n_gelu == I; returns false (nothing launched) otherwise.
+// n_gelu == I; returns false (nothing launched) otherwise. The caller
+// also guarantees the dequantisation bound of both matrices: every row
+// has 127 * sum |w| + |128 * colsum| < 2^24 (the kernel dequantises as
+// f32(acc) * sb * sa, which equals the reference's order then).
 bool mlp_block_supported(int H, int I, int KpH, int KpI, int Npi);
 bool launch_mlp_block(const MlpArgs &a, int lanes, hipStream_t s);
 // The same kernel for Wo (mlp_res.hip, WO mode): X[m] += deq(quantizeA(

@@ -26,7 +26,7 @@
 //  * the quantised g of a lane, packed 4 values a dword, is already the
 //    B operand of WoMLP for that token and K-block: the panel is written
 //    and read as whole 16-byte fragments, no transpose;
-//  * the per-channel constants (colsum, zc, sb, gamma) vary with r and
+//  * the per-channel constants (sb, gamma) vary with r and
 //    reach the lane by DPP row_newbcast folded into the VALU operation
 //    that uses them, from one register a constant ("X form": lane i holds
 //    channel (i % 16) + 16*(i / 32) of the tile).
@@ -99,12 +99,15 @@ __device__ __forceinline__ void sfor(F &&f) {
   sfor_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// Dequantisation with the channel constants in X form (the DPP folds into
-// v_add_u32, v_subrev_f32 and v_mul_f32: t + (-zc) is t - zc, signed zeros
-// included).
+// Dequantisation, ((f32(acc + 128*colsum) - zc) * sb) * sa, with sb in X
+// form (the DPP folds into the v_mul_f32). The kernel runs only for
+// weights whose every row has 127 * sum |w| + |128 * colsum| < 2^24 (the
+// host checks on upload): then acc + 128*colsum is exact in float32 for
+// any int8 activations, and so is its difference with zc = 128*colsum,
+// which is acc — so f32(tile) - zc is f32(acc) bit for bit.
 template <int R, int B = 0>
-__device__ __forceinline__ float deqx(int acc, int c1x, float zcx, float sbx, float sa) {
-  return (((float)(acc + bci<R, B>(c1x)) + (-bcf<R, B>(zcx))) * bcf<R, B>(sbx)) * sa;
+__device__ __forceinline__ float deqx(int acc, float sbx, float sa) {
+  return ((float)acc * bcf<R, B>(sbx)) * sa;
 }
 
 __device__ __forceinline__ int pack4(float a, float b, float c, float d, float inv) {
@@ -124,17 +127,19 @@ struct Shape {
   static constexpr int SP = MAXT - HOLD;           // LDS slots of the busiest wave
   static constexpr int SLOTS = RT == 0 ? NW * SP : RT * SP + (NW - RT) * (SP > 0 ? SP - 1 : 0);
   static constexpr int NJ = (HT + NW - 1) / NW;    // output tiles of the busiest wave
-  static constexpr int PF1 = 4;                    // Wi K steps in flight
-  static constexpr int PF2 = 4;                    // WoMLP K steps in flight
+  // Wi K steps in flight (the ring's slot of step kt is kt % PF1 across
+  // tiles, so PF1 divides KT1)
+  static constexpr int PF1 = KT1 % 3 == 0 ? 3 : 4;
+  static constexpr int PF2 = 3;                    // WoMLP K steps in flight
   static constexpr int SWC = NW * 32;             // channels a stage of x: tile j of every wave
   static constexpr int XST = SWC + 8;              // floats a staged row (chains conflict-free)
   static constexpr int IN = BM * H;                // the input rows, fragment order
   static constexpr int SLOT = 2 * 16 * 64 * 4;     // one tile of g (64 tokens x 32 channels)
   static constexpr int PANEL = BM * I;
   static constexpr int XS = BM * XST * 4;
-  static constexpr int SMEM = std::max(std::max(IN + SLOTS * SLOT, PANEL), XS);
+  static constexpr int SMEM = std::max(std::max(IN + SLOTS * SLOT, PANEL), (NJ > 1 ? 2 : 1) * XS);
   static_assert(H % 128 == 0 && I % 32 == 0, "shape: stages of whole 128-channel pieces");
-  static_assert(KT1 >= PF1 && KT2 >= PF2, "prefetch depth");
+  static_assert(KT1 >= PF1 && KT2 >= PF2 && KT1 % PF1 == 0, "prefetch depth");
   static_assert(SMEM <= 150 * 1024, "LDS");
 };
 
@@ -148,7 +153,7 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
   int8_t *const in_s = smem;               // W: input fragments [KT1][2][64][16]
   float *const slot_s = (float *)(smem + S::IN);  // W, Q: spilled g tiles
   int8_t *const panel = smem;              // Q, M: [KT2][2][64][16]
-  float *const xs = (float *)smem;         // R: a stage of the rows [BM][XST]
+  float *const xs = (float *)smem;         // R: stages of the rows [2][BM][XST]
   __shared__ __attribute__((aligned(16))) float rmax_s[BM][NW];
   __shared__ float mean_s[BM], rstd_s[BM];
 
@@ -187,7 +192,12 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
   for (int b = 0; b < 2; b++) sa_t[b] = 32 * b + fr < rows ? a.sa[m0 + 32 * b + fr] : 0.f;
 
   // ---- W. Wi + GeGLU ----
-  const int ntile = (NG - wave + NW - 1) / NW;  // MAXT or MAXT - 1
+  // gated tiles are dealt by wave (gw), the extra ones (NG % 8 != 0) to
+  // waves 0 .. RT-1: a SIMD runs waves s and s + 4 and issues the older
+  // one's instructions first (dealt to the younger wave instead, the extra
+  // tile measured slower)
+  const int gw = wave;
+  const int ntile = (NG - gw + NW - 1) / NW;  // MAXT or MAXT - 1
   const int skip = MAXT - ntile;                // virtual tiles this wave skips (0 or 1)
   const auto wrs = buf_rsrc(a.Bi, (uint32_t)KT1 * a.Npi * 32);
   // weight fragments of gated tile t, K step kt: the GELU-input rows and
@@ -199,40 +209,69 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
   };
   v4i wq[PF1][2];
 #pragma unroll
-  for (int s = 0; s < PF1; s++) loadW(wave, s, wq[s]);
+  for (int s = 0; s < PF1; s++) loadW(gw, s, wq[s]);
   lds_barrier();  // the input fragments are in LDS
 
   float gh[HOLD][2][16];  // the wave's last HOLD tiles of g
   float gmx[2] = {0.f, 0.f};  // max |g| of this lane's two tokens
+  // The GeGLU of a tile runs inside the next tile's K loop, a value or two
+  // a K step, so that every wave issues MFMAs and VALU work together (one
+  // wave alone issues VALU at about half the SIMD's rate, two waves
+  // together at its full rate): pacc and psb hold the previous tile's
+  // accumulators and column scales. Zero before the first tile: a wave
+  // with MAXT - 1 tiles runs that GeGLU on zeros and stores nothing.
+  v16i pacc[4] = {};
+  float psba[2] = {0.f, 0.f}, psbb[2] = {0.f, 0.f};
+  float pg[2][16];  // g of a tile bound for LDS, four values at a time
+  // LDS slot of virtual tile k (k < MAXT - HOLD; the wave has it)
+  auto slot_of = [&](int k) {
+    return RT == 0 ? gw * SP + k : (gw < RT ? gw * SP + k : RT * SP + (gw - RT) * (SP - 1) + k - 1);
+  };
+  // GeGLU (GeluMul, vec_simd.go:125-160; every gated column takes the FMA
+  // form: n_gelu == I) of value v of virtual tile KP: token block v / 16,
+  // channel 16*fh + v % 16
+  auto geglu_v = [&](auto kpv, auto vv) {
+    constexpr int KP = decltype(kpv)::value, v = decltype(vv)::value, b = v / 16, r = v % 16;
+    const float za = deqx<r, b>(pacc[b][r], psba[b], sa_t[b]);
+    const float zb = deqx<r, b>(pacc[2 + b][r], psbb[b], sa_t[b]);
+    const float g = gelu_fma(za) * zb;
+    gmx[b] = amax(gmx[b], g);
+    if constexpr (KP >= MAXT - HOLD) {
+      gh[KP - (MAXT - HOLD)][b][r] = g;
+    } else {
+      pg[b][r] = g;
+      if constexpr (r % 4 == 3) {
+        // the wave's LDS slot: [b][r/4][64 lanes][4]
+        if (KP >= skip)  // wave-uniform: the tile exists
+          *(float4 *)(slot_s + slot_of(KP) * (S::SLOT / 4) + lane * 4 + (b * 4 + r / 4) * 256) =
+              make_float4(pg[b][r - 3], pg[b][r - 2], pg[b][r - 1], pg[b][r]);
+      }
+    }
+  };
   sfor<MAXT>([&](auto kv) {
     constexpr int k = decltype(kv)::value;
     if (k < skip) return;  // wave-uniform
-    const int t = wave + NW * (k - skip);
-    // channel constants of the tile in X form (loaded before this tile's
-    // refills: loads retire in order)
+    const int t = gw + NW * (k - skip);
+    // column scales of the tile in X form (loaded before this tile's
+    // refills: loads retire in order); token block 1 takes its own copy
+    // (read at ca + dup, dup == 0 but opaque), so that each block's DPP
+    // broadcasts fold into their uses instead of one v_mov_b32_dpp shared
+    // by both
     const int ca = 64 * t + xi, cb = ca + 32;
-    // token block 1 takes its own copy (read at ca + dup, dup == 0 but
-    // opaque), so that each block's DPP broadcasts fold into their uses
-    // instead of one v_mov_b32_dpp shared by both
-    int c1a[2], c1b[2];
-    float zca[2], sba[2], zcb[2], sbb[2];
+    float sba[2], sbb[2];
 #pragma unroll
     for (int b = 0; b < 2; b++) {
       const int o = b ? dup : 0;
-      c1a[b] = a.c128i[ca + o];
-      c1b[b] = a.c128i[cb + o];
-      zca[b] = a.zci[ca + o];
       sba[b] = a.sbi[ca + o];
-      zcb[b] = a.zci[cb + o];
       sbb[b] = a.sbi[cb + o];
     }
     v16i acc[4];  // [GELU input | multiplier][token block]
     const int8_t *bp = in_s + lane * 16;
     v4i b0 = *(const v4i *)bp, b1 = *(const v4i *)(bp + 1024);
-#pragma unroll
-    for (int kt = 0; kt < KT1; kt++) {
+    sfor<KT1>([&](auto ktv) {
+      constexpr int kt = decltype(ktv)::value;
       v4i n0 = b0, n1 = b1;
-      if (kt + 1 < KT1) {
+      if constexpr (kt + 1 < KT1) {
         n0 = *(const v4i *)(bp + (kt + 1) * 2048);
         n1 = *(const v4i *)(bp + (kt + 1) * 2048 + 1024);
       }
@@ -242,54 +281,28 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
       acc[2] = mfma32(w[1], b0, kt == 0 ? v16i{} : acc[2]);
       acc[3] = mfma32(w[1], b1, kt == 0 ? v16i{} : acc[3]);
       // this slot's next step: this tile's, else the next tile's
-      if (kt + PF1 < KT1) loadW(t, kt + PF1, wq[kt % PF1]);
+      if constexpr (kt + PF1 < KT1) loadW(t, kt + PF1, wq[kt % PF1]);
       else loadW(t + NW, kt + PF1 - KT1, wq[kt % PF1]);
+      // the previous tile's GeGLU values of this step
+      if constexpr (k >= 1) {
+        sfor<32>([&](auto vv) {
+          if constexpr (decltype(vv)::value * KT1 / 32 == kt) geglu_v(std::integral_constant<int, k - 1>{}, vv);
+        });
+      }
       b0 = n0;
       b1 = n1;
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // GeGLU (GeluMul, vec_simd.go:125-160; every gated column takes the
-    // FMA form: n_gelu == I) of token block b, channel 16*fh + r
-    float g[2][16];
-    sfor<2>([&](auto bv) {
-      constexpr int b = decltype(bv)::value;
-      sfor<16>([&](auto rv) {
-        constexpr int r = decltype(rv)::value;
-        const float za = deqx<r, b>(acc[b][r], c1a[b], zca[b], sba[b], sa_t[b]);
-        const float zb = deqx<r, b>(acc[2 + b][r], c1b[b], zcb[b], sbb[b], sa_t[b]);
-        g[b][r] = gelu_fma(za) * zb;
-        gmx[b] = amax(gmx[b], g[b][r]);
-      });
+      __builtin_amdgcn_sched_barrier(0);  // keep the refill and the GeGLU values at their step
     });
-    if constexpr (k >= MAXT - HOLD) {
 #pragma unroll
-      for (int b = 0; b < 2; b++)
+    for (int q = 0; q < 4; q++) pacc[q] = acc[q];
 #pragma unroll
-        for (int r = 0; r < 16; r++) gh[k - (MAXT - HOLD)][b][r] = g[b][r];
-    } else {
-      // the wave's LDS slot k - skip: [b][r/4][64 lanes][4]
-      const int slot = RT == 0 ? wave * SP + k : (wave < RT ? wave * SP + k : RT * SP + (wave - RT) * (SP - 1) + k - 1);
-      float *sp = slot_s + slot * (S::SLOT / 4) + lane * 4;
-#pragma unroll
-      for (int b = 0; b < 2; b++)
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-          *(float4 *)(sp + (b * 4 + q) * 256) = make_float4(g[b][4 * q], g[b][4 * q + 1], g[b][4 * q + 2], g[b][4 * q + 3]);
+    for (int b = 0; b < 2; b++) {
+      psba[b] = sba[b];
+      psbb[b] = sbb[b];
     }
   });
-
-  // The x rows move between HBM and LDS in stages of SWC channels (tile j
-  // of every wave), a row's stage as whole 1 KB pieces: wave w loads rows
-  // 8w .. 8w+7, lane l floats 4l .. 4l+3 (rows past M read 0). Stage 0's
-  // loads are issued here, ahead of Q and M, whose first waits they join.
-  const auto xrs = buf_rsrc(a.X + (size_t)m0 * H, (uint32_t)rows * H * 4);
-  auto load_stage = [&](int s, v4i *dst) {
-#pragma unroll
-    for (int u = 0; u < 8; u++)
-      dst[u] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (uint32_t)(((8 * wave + u) * H + SWC * s + 4 * lane) * 4), 0, 0);
-  };
-  v4i xin[8];
-  load_stage(0, xin);
+  // the last tile's GeGLU (every wave has virtual tile MAXT - 1)
+  sfor<32>([&](auto vv) { geglu_v(std::integral_constant<int, MAXT - 1>{}, vv); });
 
   // WoMLP weight fragments of the first PF2 K steps (independent of g): in
   // flight during Q. Wave w's output tiles: c = w + NW*j (j < NJ, c < HT).
@@ -338,7 +351,7 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
 #pragma unroll
   for (int k = 0; k < SP; k++) {
     if (k < skip) continue;
-    const int slot = RT == 0 ? wave * SP + k : (wave < RT ? wave * SP + k : RT * SP + (wave - RT) * (SP - 1) + k - 1);
+    const int slot = slot_of(k);
     const float *sp = slot_s + slot * (S::SLOT / 4) + lane * 4;
 #pragma unroll
     for (int b = 0; b < 2; b++)
@@ -353,7 +366,7 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
   sfor<MAXT>([&](auto kv) {
     constexpr int k = decltype(kv)::value;
     if (k < skip) return;
-    const int t = wave + NW * (k - skip);
+    const int t = gw + NW * (k - skip);
 #pragma unroll
     for (int b = 0; b < 2; b++) {
       v4i v;
@@ -364,18 +377,28 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
   });
   lds_barrier();
 
+  // The x rows move between HBM and LDS in stages of SWC channels (tile j
+  // of every wave), a row's stage as whole 1 KB pieces: wave w loads rows
+  // 8w .. 8w+7, lane l floats 4l .. 4l+3 (rows past M read 0). The first
+  // two stages' loads are issued here, in flight during M, stage s + 2's
+  // while stage s is processed: spread over the block, x's HBM traffic
+  // does not come in one burst from every CU at once.
+  const auto xrs = buf_rsrc(a.X + (size_t)m0 * H, (uint32_t)rows * H * 4);
+  auto load_stage = [&](int s, v4i *dst) {
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      dst[u] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (uint32_t)(((8 * wave + u) * H + SWC * s + 4 * lane) * 4), 0, 0);
+  };
+  v4i xin[NJ > 1 ? 2 : 1][8];
+  load_stage(0, xin[0]);
+  if constexpr (NJ > 1) load_stage(1, xin[1]);
+
   // ---- M. WoMLP ----
-  int c1o[NJ][2];
-  float zco[NJ][2], sbo[NJ][2];
+  float sbo[NJ][2];
 #pragma unroll
   for (int j = 0; j < NJ; j++)
 #pragma unroll
-    for (int b = 0; b < 2; b++) {
-      const int col = 32 * min(wave + NW * j, HT - 1) + xi + (b ? dup : 0);
-      c1o[j][b] = a.c128o[col];
-      zco[j][b] = a.zco[col];
-      sbo[j][b] = a.sbo[col];
-    }
+    for (int b = 0; b < 2; b++) sbo[j][b] = a.sbo[32 * min(wave + NW * j, HT - 1) + xi + (b ? dup : 0)];
   v16i acc[NJ][2];
   {
     const int8_t *pp = panel + lane * 16;
@@ -418,7 +441,10 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
   double pd = 0.0;
 #pragma unroll
   for (int u = 0; u < CPT; u++) p[u] = 0.f;
-  // the chains over the columns of stage s in xs (pass 0: sums; 1: d*d)
+  // stage s lives in buffer s % NBUF of xs
+  constexpr int NBUF = NJ > 1 ? 2 : 1;
+  auto xsb = [&](int s) { return xs + (s % NBUF) * (BM * XST); };
+  // the chains over the columns of stage s (pass 0: sums; 1: d*d)
   auto chains = [&](int s, int pass) {
     const int scw = min(SWC, H - SWC * s);  // channels of the stage (a multiple of 128)
     if constexpr (V > 0) {
@@ -426,7 +452,7 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
       for (int u = 0; u < CPT; u++) {
         const int ch = tid + 512 * u;
         if (ch < NCH) {
-          const float *xr = xs + (ch / V) * XST + ch % V;
+          const float *xr = xsb(s) + (ch / V) * XST + ch % V;
           // NB reads issued before their NB adds (the sums stay in column
           // order)
           auto batch = [&](int e0, auto nb) {
@@ -452,7 +478,7 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
         }
       }
     } else if (tid < BM) {
-      const float *xr = xs + tid * XST;
+      const float *xr = xsb(s) + tid * XST;
       if (pass == 0) {
         for (int e = 0; e < scw; e++) pd += (double)xr[e];
       } else {
@@ -483,29 +509,43 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
     }
     pd = 0.0;
   };
-  // this wave's 16 values of stage s, token block b, in xs
-  auto xs_own = [&](int b) { return xs + (32 * b + fr) * XST + 32 * wave + 16 * fh; };
+  // this wave's 16 values of stage s, token block b
+  auto xs_own = [&](int s, int b) { return xsb(s) + (32 * b + fr) * XST + 32 * wave + 16 * fh; };
+  auto put_own = [&](int s) {  // x of stage s from registers into its buffer
+    if (wave + NW * s < HT) {
 #pragma unroll
-  for (int s = 0; s < NJ; s++) {
+      for (int b = 0; b < 2; b++) {
+        float *xo = xs_own(s, b);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          *(float4 *)(xo + 4 * q) = make_float4(x[s][b][4 * q], x[s][b][4 * q + 1], x[s][b][4 * q + 2], x[s][b][4 * q + 3]);
+      }
+    }
+  };
+  lds_barrier();  // every wave is past the panel (M)
+  sfor<NJ>([&](auto sv) {
+    constexpr int s = decltype(sv)::value;
     const int scw = min(SWC, H - SWC * s);
     const bool own = wave + NW * s < HT;  // wave-uniform: tile w + 8s exists
-    lds_barrier();  // every wave is past the panel (M) or the previous stage's chains
+    // (the buffer's previous stage, s - 2, was read before stage s - 1's
+    // barriers)
+    float *const xb = xsb(s);
 #pragma unroll
     for (int u = 0; u < 8; u++)
-      if (4 * lane < scw) *(v4i *)(xs + (8 * wave + u) * XST + 4 * lane) = xin[u];
-    if (s + 1 < NJ) load_stage(s + 1, xin);
+      if (4 * lane < scw) *(v4i *)(xb + (8 * wave + u) * XST + 4 * lane) = xin[s % 2][u];
+    if constexpr (s + 2 < NJ) load_stage(s + 2, xin[s % 2]);
     lds_barrier();
     if (own) {
       sfor<2>([&](auto bv) {
         constexpr int b = decltype(bv)::value;
-        float *xo = xs_own(b);
+        float *xo = xs_own(s, b);
         float4 v[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) v[q] = *(const float4 *)(xo + 4 * q);
         sfor<16>([&](auto rv) {
           constexpr int r = decltype(rv)::value;
           const float xv = r % 4 == 0 ? v[r / 4].x : r % 4 == 1 ? v[r / 4].y : r % 4 == 2 ? v[r / 4].z : v[r / 4].w;
-          x[s][b][r] = xv + deqx<r, b>(acc[s][b][r], c1o[s][b], zco[s][b], sbo[s][b], gs[b]);
+          x[s][b][r] = xv + deqx<r, b>(acc[s][b][r], sbo[s][b], gs[b]);
         });
 #pragma unroll
         for (int q = 0; q < 4; q++)
@@ -517,28 +557,28 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; u++)
       if (4 * lane < scw)
-        __builtin_amdgcn_raw_buffer_store_b128(*(const v4i *)(xs + (8 * wave + u) * XST + 4 * lane), xrs,
+        __builtin_amdgcn_raw_buffer_store_b128(*(const v4i *)(xb + (8 * wave + u) * XST + 4 * lane), xrs,
                                                (uint32_t)(((8 * wave + u) * H + SWC * s + 4 * lane) * 4), 0, 0);
     if constexpr (LN) chains(s, 0);
-  }
+  });
   if constexpr (!LN) return;
   combine(0);
-  // the variance pass: the stages again, from x
-#pragma unroll
-  for (int s = 0; s < NJ; s++) {
-    const bool own = wave + NW * s < HT;
-    lds_barrier();  // the chains are past the previous stage
-    if (own) {
-#pragma unroll
-      for (int b = 0; b < 2; b++) {
-        float *xo = xs_own(b);
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-          *(float4 *)(xo + 4 * q) = make_float4(x[s][b][4 * q], x[s][b][4 * q + 1], x[s][b][4 * q + 2], x[s][b][4 * q + 3]);
-      }
-    }
+  // the variance pass, the stages again in column order: the last two are
+  // still in their buffers, unless an earlier stage is written over one
+  // (three stages: stage 0 goes over stage 2, which comes back after)
+  if constexpr (NJ <= 2) {
+    sfor<NJ>([&](auto sv) { chains(decltype(sv)::value, 1); });
+  } else {
+    static_assert(NJ == 3, "stages");
+    lds_barrier();  // the sums' chains are past stage 2
+    put_own(0);
     lds_barrier();
-    chains(s, 1);
+    chains(0, 1);
+    chains(1, 1);
+    lds_barrier();  // past stage 0's buffer
+    put_own(2);
+    lds_barrier();
+    chains(2, 1);
   }
   combine(1);
 #pragma unroll
@@ -643,6 +683,8 @@ bool launch_ln(const MlpArgs &a, int lanes, hipStream_t s) {
 
 }  // namespace mlp_block_impl
 
+// (the caller also checks that Wi and WoMLP hold the dequantisation bound
+// above: Mat::small on the host)
 bool mlp_block_supported(int H, int I, int KpH, int KpI, int Npi) {
   if (KpH != H || KpI != I || Npi != 2 * I) return false;
   return (H == 768 && I == 1152) || (H == 384 && I == 1152) || (H == 256 && I == 512);

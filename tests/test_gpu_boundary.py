@@ -252,7 +252,7 @@ def test_option_values_checked():
     cfg = small_cfg(layers=1)
     w, gpu, _ = _pair(cfg, seed=47)
     for name, bad in (("parts", 5), ("qkv_heads", 3), ("gemm", 3), ("gemm_tile", -1), ("pass_tokens", 0),
-                      ("fuse_res", 5), ("fuse_mlp", 2), ("qkv_kblock", 2)):
+                      ("fuse_res", 5), ("fuse_mlp", 3), ("qkv_kblock", 2)):
         with pytest.raises(_lib.IxhError, match="out of range"):
             gpu.set_option(name, bad)
     gpu.set_option("parts", 2)

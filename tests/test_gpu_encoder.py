@@ -334,6 +334,28 @@ def test_mlp_block_lanes(lanes):
         assert f32_bits_equal(got, want), (shape, mismatch_report(got, want))
 
 
+@pytest.mark.parametrize("which", ["wi", "womlp"])
+def test_mlp_block_bound_fallback(which):
+    """A weight row past the 64-row kernel's dequantisation bound (127 *
+    sum|w| + |128 * colsum| >= 2^24: a row of 127s) sends the MLP block to
+    the exact kernels; the result is the oracle's either way, with the
+    tokens aligned to that row so that its tiles pass 2^24."""
+    for shape in ("small", "base"):
+        cfg = _shape_cfg(shape, 2)
+        w = Weights.random(cfg, seed=89)
+        m = w.wi_q if which == "wi" else w.womlp_q
+        m[0, 3, :] = 127
+        gpu, ora = Model(w, lanes=8), orc.OracleModel(w, lanes=8)
+        rng = np.random.default_rng(89)
+        seqs = ids_uniform_lengths(rng, 6, 1, 200, cfg.vocab)
+        want, _ = ora.encode_tokens(seqs)
+        for mlp in (2, 1):
+            with options(gpu, fuse_mlp=mlp):
+                got = gpu.encode_tokens(seqs)
+            assert f32_bits_equal(got, want), (shape, mlp, mismatch_report(got, want))
+        gpu.close()
+
+
 def test_bekko_width_exact():
     """The reference's own backbone width (bekko a8m: hidden 384, 6 heads,
     MLP 2 x 1152; linalg/gemm_test.go:104-105) through the whole encoder,
