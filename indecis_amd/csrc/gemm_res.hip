@@ -242,17 +242,29 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; r++) x[j][r] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(xrs, vo, roff(r), 0));
   }
+  // (with the weights' bound, checked on upload, f32(acc + 128 colsum) -
+  // zc is f32(acc) exactly)
+  const bool small = a.small;
 #pragma unroll
   for (int j = 0; j < NB; j++) {
     const int col = cb + 32 * j + fr;
     const int c1 = a.c128[col];
     const float zc = a.zc[col], sb = a.sb[col];
     const uint32_t vo = (uint32_t)(4 * fh * H + col) * 4;
+    if (small) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const float v = deq(acc[j][r] + c1, zc, sb, sa_s[acc_row(r, lane)]);
-      x[j][r] = x[j][r] + v;
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x[j][r]), xrs, vo, roff(r), 0);
+      for (int r = 0; r < 16; r++) {
+        const float v = ((float)acc[j][r] * sb) * sa_s[acc_row(r, lane)];
+        x[j][r] = x[j][r] + v;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x[j][r]), xrs, vo, roff(r), 0);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const float v = deq(acc[j][r] + c1, zc, sb, sa_s[acc_row(r, lane)]);
+        x[j][r] = x[j][r] + v;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x[j][r]), xrs, vo, roff(r), 0);
+      }
     }
   }
   if constexpr (!LN) return;

@@ -809,6 +809,7 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
     g.lanes = c.lanes;
     g.n_gelu = gelu_fma_cols(I, c.lanes);
     g.tile_cfg = tune.gemm_tile;  // the tiled GEMM's tiles, wherever it runs
+    g.small = M.small;
     return g;
   };
   // GEMM HBM bytes: activations int8 + scales, weights, output (read too
@@ -881,6 +882,7 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
     r.Q = w->xq.as<int8_t>();
     r.ldq = KpH;
     r.SA = w->sa.as<float>();
+    r.small = M.small;
     return r;
   };
   // bytes of a fused residual GEMM: input rows f32, weights, x read and

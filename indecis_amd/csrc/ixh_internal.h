@@ -76,6 +76,11 @@ struct GemmArgs {
   float *sq;
   float attn_scale;
   int tile_cfg;  // gemm_i8: 0: 128x128 tiles, 2 LDS stages; 1: 256x128, 3; 2: 128x128, 3
+  // every weight row has 127 * sum|w| + |128 * colsum| < 2^24: the
+  // reference's f32(acc + 128*colsum) - zc is then f32(acc) for any int8
+  // activations, and kernels that read this may dequantise as
+  // f32(acc) * sb * sa (the fused QKV kernel does)
+  int small = 0;
   // EPI_GEGLU on gemm_as: when not null, rmax[m][c] = max |G[m][32c .. 32c+31]|
   // for c < rmax_ld (the row maxima the fused residual GEMM quantises by)
   float *rmax = nullptr;
@@ -126,6 +131,7 @@ struct ResArgs {
   // the fused QKV kernel's K-blocked input)
   int8_t *Qk = nullptr;
   int qk_rows = 0;
+  int small = 0;  // the weights' dequantisation bound holds (GemmArgs::small)
 };
 bool gemm_res_supported(int H, int Kp, int Np);
 bool launch_gemm_res(const ResArgs &a, int lanes, hipStream_t s);

@@ -285,11 +285,22 @@ __global__ __launch_bounds__(512 * NH, 4) void qkv_attn_kernel(GemmArgs g, AttnA
     // a block past n (stored as padding keys) is not computed: its values
     // reach only rows past n, which every store below writes as zeros
     if (wv + 8 * i >= nbc) continue;
+    if (g.small) {
+      // the weights' bound holds (checked on upload): f32(acc + 128
+      // colsum) - zc is f32(acc) exactly
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const float sa = sa_s[32 * (wv + 8 * i) + acc_row(r, lane)];
-      v[i][0][r] = deq(acc[i][0][r] + c128[0], zc[0], sb[0], sa);
-      v[i][1][r] = deq(acc[i][1][r] + c128[1], zc[1], sb[1], sa);
+      for (int r = 0; r < 16; r++) {
+        const float sa = sa_s[32 * (wv + 8 * i) + acc_row(r, lane)];
+        v[i][0][r] = ((float)acc[i][0][r] * sb[0]) * sa;
+        v[i][1][r] = ((float)acc[i][1][r] * sb[1]) * sa;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const float sa = sa_s[32 * (wv + 8 * i) + acc_row(r, lane)];
+        v[i][0][r] = deq(acc[i][0][r] + c128[0], zc[0], sb[0], sa);
+        v[i][1][r] = deq(acc[i][1][r] + c128[1], zc[1], sb[1], sa);
+      }
     }
   }
   if (rope) {

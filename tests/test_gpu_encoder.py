@@ -334,16 +334,18 @@ def test_mlp_block_lanes(lanes):
         assert f32_bits_equal(got, want), (shape, mismatch_report(got, want))
 
 
-@pytest.mark.parametrize("which", ["wi", "womlp"])
-def test_mlp_block_bound_fallback(which):
-    """A weight row past the 64-row kernel's dequantisation bound (127 *
-    sum|w| + |128 * colsum| >= 2^24: a row of 127s) sends the MLP block to
-    the exact kernels; the result is the oracle's either way, with the
-    tokens aligned to that row so that its tiles pass 2^24."""
+@pytest.mark.parametrize("which", ["wi", "womlp", "wqkv", "wo"])
+def test_deq_bound_fallback(which):
+    """A weight row past the dequantisation bound (127 * sum|w| + |128 *
+    colsum| >= 2^24: a row of 127s) makes the kernels that dequantise as
+    f32(acc) * sb * sa take the reference's order for that matrix (the
+    64-row MLP kernel hands the block to the exact kernels; the fused QKV
+    and Wo kernels switch their epilogue); the result is the oracle's
+    either way."""
     for shape in ("small", "base"):
         cfg = _shape_cfg(shape, 2)
         w = Weights.random(cfg, seed=89)
-        m = w.wi_q if which == "wi" else w.womlp_q
+        m = {"wi": w.wi_q, "womlp": w.womlp_q, "wqkv": w.wqkv_q, "wo": w.wo_q}[which]
         m[0, 3, :] = 127
         gpu, ora = Model(w, lanes=8), orc.OracleModel(w, lanes=8)
         rng = np.random.default_rng(89)
