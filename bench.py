@@ -179,6 +179,47 @@ def serving(np, model, cfg, args):
     }), flush=True)
 
 
+def spans(np, model, cfg, seqs, args):
+    """The token-level spans head of cfg3 and cfg5 (BIO over 4 span types:
+    9 logits a token, spanTagCount spans.go:125; logits spans.go:449-459)
+    on every token of the batch, in the encoder pass (ixh_encode_heads:
+    host ids in, host float64 logits out, mean pooling as infer pools with
+    Spans questions, spans.go:466-476). Reports the call's rate and the head
+    kernel's HBM rate from its HIP events (its algorithmic bytes: each
+    token's float32 state in, 9 float64 logits out, the weights once)."""
+    from indecis_amd import heads as hd
+    rng = np.random.default_rng(11)
+    rows = hd.span_tag_count(4)
+    w, b = hd.random_head(rows, cfg.hidden, rng)
+    model.set_heads([(w, b, True)])
+    N = sum(len(s) for s in seqs)
+    model.encode_heads(seqs, mean=True, pooled=False)  # warm-up: workspaces
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        model.encode_heads(seqs, mean=True, pooled=False)
+    dt = (time.perf_counter() - t0) / args.steps
+    model.set_profiling(True, only="head_tokens")
+    for _ in range(args.steps):
+        model.encode_heads(seqs, mean=True, pooled=False)
+    st = model.profile()["head_tokens"]
+    model.set_profiling(False)
+    avg_s = st["ms"] / st["launches"] / 1e3
+    per_launch = st["bytes"] / st["launches"]
+    gbs = per_launch / avg_s / 1e9
+    line = {
+        "metric": "spans head logits on every token, with the encoder pass (host ids in, host logits out)",
+        "value": round(N / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "ms_per_call": round(dt * 1e3, 3), "higher_is_better": True, "dtype": "int8 encoder, f64 head sums",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "tokens": N, "sequences": len(seqs), "hidden": cfg.hidden,
+                   "head_rows": rows},
+        "head_kernel": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                        "frac": round(gbs * 1e9 / PEAK_HBM, 4), "avg_launch_us": round(avg_s * 1e6, 2),
+                        "launches_timed": st["launches"], "algorithmic_bytes_per_launch": per_launch},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def decide(np, model, cfg, args):
     """DecideInputs-shaped load (model.go:316-330, spans.go:369-383): many
     short inputs, each through the encoder and three pooled-row heads
@@ -399,6 +440,8 @@ def main():
     ap.add_argument("--tokenize", action="store_true",
                     help="instead: host tokenizer throughput, and text to pooled rows for one batch")
     ap.add_argument("--docs", type=int, default=4096, help="documents (--tokenize)")
+    ap.add_argument("--spans", action="store_true",
+                    help="instead: the workload's token-level spans head (9 logits a token) in the pass")
     ap.add_argument("--decide", action="store_true",
                     help="instead: a DecideInputs-shaped load, 32-sequence passes vs heads on the device")
     ap.add_argument("--inputs", type=int, default=8192, help="inputs (--decide)")
@@ -446,6 +489,10 @@ def main():
         return
     if args.decide:
         decide(np, model, cfg, args)
+        model.close()
+        return
+    if args.spans:
+        spans(np, model, cfg, seqs, args)
         model.close()
         return
     ids_d = torch.from_numpy(np.concatenate(seqs)).to("cuda")

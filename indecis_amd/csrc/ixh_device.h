@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace ixh {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -232,6 +234,18 @@ __device__ __forceinline__ float wave_max(float x) {
   const int h = __float_as_int(halfwave_max(x));
   return __builtin_fmaxf(__int_as_float(__builtin_amdgcn_readlane(h, 31)),
                          __int_as_float(__builtin_amdgcn_readlane(h, 63)));
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), in
+// order: a loop whose index is a constant in every body (register arrays
+// indexed by it stay in registers).
+template <typename F, int... I>
+__device__ __forceinline__ void sfor_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void sfor(F &&f) {
+  sfor_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 // Dequantisation of one int8 GEMM result (kernel_vnni_amd64.s:144-200):

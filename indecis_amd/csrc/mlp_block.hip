@@ -89,16 +89,6 @@ __device__ __forceinline__ float bcf(float v) {
   return __int_as_float(bci<N, B>(__float_as_int(v)));
 }
 
-template <typename F, int... I>
-__device__ __forceinline__ void sfor_impl(F &&f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), in order
-template <int N, typename F>
-__device__ __forceinline__ void sfor(F &&f) {
-  sfor_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 // Dequantisation, ((f32(acc + 128*colsum) - zc) * sb) * sa, with sb in X
 // form (the DPP folds into the v_mul_f32). The kernel runs only for
 // weights whose every row has 127 * sum |w| + |128 * colsum| < 2^24 (the

@@ -567,16 +567,114 @@ __global__ void pool_kernel(const float *xn, const int32_t *offs, int H, int cls
 }
 
 // heads.go:63-74: z = sum f64(w)*f64(x), in order, + f64(b).
-__global__ void head_logits_kernel(const float *x, int T, int H, const float *w, const float *b,
-                                   int rows, double *z) {
-  const int g = blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= T * rows) return;
-  const int t = g / rows, r = g % rows;
-  const float *xr = x + (size_t)t * H;
-  const float *wr = w + (size_t)r * H;
-  double s = 0.0;
-  for (int i = 0; i < H; i++) s += (double)wr[i] * (double)xr[i];
-  z[g] = s + (double)b[r];
+// head.logits (heads.go:63-74) and the spans head (spans.go:449-459):
+// z[t][r] = sum_i f64(w[r][i]) * f64(x[t][i]) in column order, + f64(b[r]).
+// Each product of two float32 is exact in float64, so fma(x, w, s) rounds
+// once where the reference's s + x*w does: the same bits. One workgroup of
+// 4 waves takes HL_T tokens (lane l: tokens l and l + 64) and up to rg <=
+// HL_R rows (wave w the rows r0 + w, r0 + w + 4, ...: at most 2 HL_R / 4
+// chains a thread, each weight read from LDS serving two of them;
+// more rows take more workgroups along y, each reading x again); the rows'
+// weights sit in LDS widened to float64 (every lane of a wave reads the
+// same one: a broadcast); x comes through LDS in chunks of HL_C columns,
+// loaded as whole 128-byte pieces of its rows (8 threads a token) HL_PD
+// chunks ahead.
+constexpr int HL_T = 128, HL_R = 12, HL_C = 32, HL_XLD = HL_C + 4, HL_PD = 2;
+constexpr int HL_WMAX = 16384;  // float64 weights a workgroup holds (rg * H <= HL_WMAX: 128 KB)
+constexpr int HL_RW = HL_R / 4;  // chains a thread a token
+static_assert(64 % (HL_PD * HL_C) == 0, "every width (a multiple of 64) is whole rounds of the ring");
+__global__ __launch_bounds__(256) void head_logits_kernel(const float *x, int T, int H, const float *w,
+                                                          const float *b, int rows, int rg, double *z) {
+  extern __shared__ __attribute__((aligned(16))) double hl_w[];  // [rg][H]
+  __shared__ __attribute__((aligned(16))) float xs[HL_T * HL_XLD];
+  typedef float v4f __attribute__((ext_vector_type(4)));  // (an array of HIP's float4 struct stays in memory)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t0 = blockIdx.x * HL_T, r0 = blockIdx.y * rg;
+  const int nr = min(rg, rows - r0);
+  const int nt = min(HL_T, T - t0);
+  // the weights, float4 a thread a round, every load issued before the
+  // first conversion; rounds past the rows' end repeat the last float4
+  // (the same values to the same place: no branch)
+  {
+    constexpr int WR = HL_WMAX / 4 / 256;  // rounds at the largest rg * H
+    const int n4 = nr * H / 4;
+    v4f wv[WR];
+    sfor<WR>([&](auto kv) { wv[kv.value] = *(const v4f *)(w + (size_t)r0 * H + 4 * min(tid + 256 * kv.value, n4 - 1)); });
+    sfor<WR>([&](auto kv) {
+      const int i = min(tid + 256 * kv.value, n4 - 1);
+      *(double2 *)(hl_w + 4 * i) = make_double2((double)wv[kv.value].x, (double)wv[kv.value].y);
+      *(double2 *)(hl_w + 4 * i + 2) = make_double2((double)wv[kv.value].z, (double)wv[kv.value].w);
+    });
+  }
+  // chunk loads: piece p = tid + 256 k of the chunk's HL_T x HL_C floats,
+  // token p / 8, float4 p % 8 (tokens past T read token T-1, unused); past
+  // the last chunk the loads read the last one again (unused)
+  constexpr int PPT = HL_T * HL_C / 4 / 256;  // float4 pieces a thread
+  v4f nx[HL_PD][PPT];
+  const float *xp[PPT];
+  sfor<PPT>([&](auto kv) {
+    const int p = tid + 256 * kv.value;
+    xp[kv.value] = x + (size_t)(t0 + min(p / 8, nt - 1)) * H + 4 * (p % 8);
+  });
+  auto load = [&](int c0, auto uv) {
+    sfor<PPT>([&](auto kv) { nx[uv.value][kv.value] = *(const v4f *)(xp[kv.value] + min(c0, H - HL_C)); });
+  };
+  // chains: tokens lane and lane + 64, rows wave + 4j (a row past nr is
+  // computed on row nr - 1 and not stored: no branch in the loop)
+  double acc[2][HL_RW];
+  int roff[HL_RW];
+#pragma unroll
+  for (int j = 0; j < HL_RW; j++) {
+    acc[0][j] = acc[1][j] = 0.0;
+    roff[j] = min(wave + 4 * j, nr - 1) * H;
+  }
+  sfor<HL_PD>([&](auto uv) { load(HL_C * uv.value, uv); });
+  auto chunk = [&](int cb, auto uv) {
+      constexpr int u = decltype(uv)::value;
+      const int c0 = cb + HL_C * u;
+
+      __syncthreads();  // the previous chunk is read (and, first, the weights are in)
+      sfor<PPT>([&](auto kv) {
+        const int p = tid + 256 * kv.value;
+        *(v4f *)(xs + (p / 8) * HL_XLD + 4 * (p % 8)) = nx[u][kv.value];
+      });
+      load(c0 + HL_PD * HL_C, uv);
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < HL_C; i += 4) {
+        double xd[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const float4 v = *(const float4 *)(xs + (lane + 64 * h) * HL_XLD + i);
+          xd[h][0] = (double)v.x;
+          xd[h][1] = (double)v.y;
+          xd[h][2] = (double)v.z;
+          xd[h][3] = (double)v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < HL_RW; j++) {
+          const double *wr = hl_w + roff[j] + c0 + i;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const double wv = wr[e];
+            acc[0][j] = __builtin_fma(xd[0][e], wv, acc[0][j]);
+            acc[1][j] = __builtin_fma(xd[1][e], wv, acc[1][j]);
+          }
+        }
+      }
+  };
+  for (int cb = 0; cb < H; cb += HL_PD * HL_C) sfor<HL_PD>([&](auto uv) { chunk(cb, uv); });
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int tk = lane + 64 * h;
+    if (tk < nt) {
+#pragma unroll
+      for (int j = 0; j < HL_RW; j++) {
+        const int r = wave + 4 * j;
+        if (r < nr) z[(size_t)(t0 + tk) * rows + r0 + r] = acc[h][j] + (double)b[r0 + r];
+      }
+    }
+  }
 }
 
 // Launches kern with min(work, the workgroups that fit on the device at
@@ -671,9 +769,20 @@ void launch_pool(const float *xn, const int32_t *offs, int B, int H, int cls, fl
 
 void launch_head_logits(const float *x, int T, int H, const float *w, const float *b, int rows,
                         double *z, hipStream_t s) {
-  const long n = (long)T * rows;
-  if (n <= 0) return;
-  head_logits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(x, T, H, w, b, rows, z);
+  if (T <= 0 || rows <= 0) return;
+  // rows a workgroup: up to HL_R whose float64 weights fit in the dynamic
+  // LDS (H a multiple of HL_C: the model's width is one of 64); fewer rows,
+  // less LDS, more workgroups a CU
+  constexpr int kMaxDyn = HL_WMAX * sizeof(double);
+  const int rg = std::max(1, std::min(std::min(HL_R, rows), HL_WMAX / H));
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void *)head_logits_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDyn);
+    attr = true;
+  }
+  const dim3 grid((unsigned)((T + HL_T - 1) / HL_T), (unsigned)((rows + rg - 1) / rg));
+  const size_t shm = (size_t)rg * H * sizeof(double);
+  head_logits_kernel<<<grid, 256, shm, s>>>(x, T, H, w, b, rows, rg, z);
 }
 
 }  // namespace ixh

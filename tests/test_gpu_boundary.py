@@ -224,6 +224,25 @@ def test_heads_on_device(pooling, mean):
     gpu.close()
 
 
+@pytest.mark.parametrize("hidden", [256, 768])
+def test_head_logits_kernel_shapes(hidden):
+    """head.logits (heads.go:63-74) on the device (ixh_head_logits): the
+    float64 sums in column order for row counts within and past one
+    workgroup's 12 rows, token counts around its 64 tokens, and rows with
+    large, tiny and cancelling values, equal the oracle's bit for bit."""
+    cfg = small_cfg(layers=1) if hidden == 256 else base_cfg(layers=1)
+    w, gpu, _ = _pair(cfg, seed=48)
+    rng = np.random.default_rng(48)
+    for T, rows in ((1, 1), (63, 9), (64, 12), (65, 13), (1000, 30), (130, 4)):
+        x = rng.standard_normal((T, hidden)).astype(np.float32)
+        x[0, :8] = [3e38, -3e38, 1e-38, -1e-38, 1.0, -1.0, 65504.0, 1e-7]
+        hw = (rng.standard_normal((rows, hidden)) * 0.02).astype(np.float32)
+        hb = rng.standard_normal(rows).astype(np.float32)
+        z = gpu.head_logits(x, hw, hb)
+        assert np.array_equal(z, orc.head_logits(x, hw, hb)), (T, rows)
+    gpu.close()
+
+
 def test_cfg5_long_sequence_exact():
     """cfg5's length: one 8,192-token sequence and a short one at base width
     through 3 layers (global, local, local): the statistics kernel and 16
