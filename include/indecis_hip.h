@@ -329,8 +329,12 @@ int ixh_matmul8(ixh_packed_b8 *b, float *c, const float *a, int m,
  * 4) bytes (plus alignment) must fit, else IXH_EINVAL with the limit. The
  * work is queued on `stream` (a hipStream_t; NULL: the null stream) and
  * the call returns without waiting. Every call on a GPU shares that GPU's
- * scratch: calls that overlap on one GPU race, so serialise them (one
- * stream, or wait between calls). */
+ * scratch, so calls on one GPU run one after another on the device: each
+ * call's work waits, on its stream, for the previous call's (an event per
+ * GPU, made when the first PackedB8 of that GPU is created, recorded after
+ * every call), whichever streams or threads issue them. A call on a stream
+ * under graph capture neither waits nor records: the graph orders it, so
+ * two captured calls must not sit on parallel branches. */
 int ixh_matmul8_noalloc(ixh_packed_b8 *b, float *d_c, int ldc, const float *d_a,
                         int lda, int m, int accumulate, void *stream);
 

@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 SO = os.path.join(HERE, "libindecis_hip.so")
-SOURCES = ["gemm_i8.hip", "gemm_as.hip", "gemm_ws.hip", "gemm_res.hip", "mlp_res.hip", "mlp_block.hip", "qkv_attn.hip", "rownorm.hip", "attention_i8.hip", "outliers.hip", "safetensors.cpp", "tokenizer.cpp", "embed.cpp", "ixh_api.cpp"]
+SOURCES = ["gemm_i8.hip", "gemm_as.hip", "gemm_ws.hip", "gemm_res.hip", "mlp_res.hip", "mlp_block.hip", "qkv_attn.hip", "rownorm.hip", "attention_i8.hip", "outliers.hip", "safetensors.cpp", "tokenizer.cpp", "embed.cpp", "host_sched.cpp", "ixh_api.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-x", "hip", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",

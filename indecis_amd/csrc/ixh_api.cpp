@@ -13,10 +13,7 @@
 #include <cstring>
 #include <memory>
 #include <mutex>
-#include <condition_variable>
-#include <deque>
 #include <string>
-#include <thread>
 #include <vector>
 
 #include "../../include/indecis_hip.h"
@@ -57,11 +54,6 @@ int fail(int code, const char *fmt, ...) {
   } while (0)
 
 inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
-
-// Upper bound of Tuning::pass_tokens, and the longest sequence one pass
-// takes: every byte offset of a pass's buffers then fits in 31 bits
-// (N * 3H * 4 bytes at H 768 is 1.2 GB).
-constexpr int kMaxPassTokensOpt = 131072;
 
 // Device buffer that grows and never shrinks.
 struct DevBuf {
@@ -241,26 +233,6 @@ struct HeadSet {
   DevBuf wp, bp, wt, bt;  // [rows][H] weights, [rows] biases
 };
 
-// What a pass writes (device pointers; null: not wanted). states [N][H]
-// final states (EncodeTokens); pooled [B][H] (EncodeSeqs); zp [B][rp]
-// pooled-row head logits; zt [N][rt] per-token head logits. mean: pool by
-// the mean whatever the config (meanRows, spans.go:466-476).
-struct Outputs {
-  float *states = nullptr;
-  float *pooled = nullptr;
-  double *zp = nullptr, *zt = nullptr;
-  int mean = 0;
-  // the outputs of sequences [b0, ...) whose first token is t0
-  Outputs at(int b0, int t0, int H, const HeadSet *hs) const {
-    Outputs o = *this;
-    if (o.states) o.states += (size_t)t0 * H;
-    if (o.pooled) o.pooled += (size_t)b0 * H;
-    if (o.zp) o.zp += (size_t)b0 * hs->rp;
-    if (o.zt) o.zt += (size_t)t0 * hs->rt;
-    return o;
-  }
-};
-
 struct Workspace {
   hipStream_t stream = nullptr;
   // tabs: the pass's small host-built tables, one copy: offs [B+1], padoff
@@ -306,8 +278,7 @@ struct ixh_model {
   std::mutex heads_mu;
   std::shared_ptr<HeadSet> heads;  // null: none set
   std::vector<std::shared_ptr<DevBuf>> rope_graveyard;
-  std::mutex pool_mu;
-  std::vector<Workspace *> pool;
+  FreeList<Workspace> pool;
   std::atomic<bool> weights_valid{true};
   std::mutex tune_mu;
   Tuning tuning;
@@ -316,7 +287,7 @@ struct ixh_model {
   std::string prof_only;  // profile only this kernel class (empty: all)
   std::vector<StatAcc> stats;
   ~ixh_model() {
-    for (Workspace *w : pool) delete w;
+    for (Workspace *w : pool.drain()) delete w;
   }
 };
 
@@ -332,76 +303,6 @@ struct ixh_packed_b8 {
 };
 
 namespace {
-
-// One option of ixh_model_set_option / ixh_packb8_set_option; model_opts:
-// the encoder options are allowed (a PackedB8 handle takes only the GEMM
-// choices).
-int set_tuning(Tuning &t, int option, int64_t v, bool model_opts) {
-  auto bad = [&]() { return fail(IXH_EINVAL, "indecis: option %d: value %lld out of range", option, (long long)v); };
-  switch (option) {
-  case IXH_OPT_GEMM:
-    if (v < 0 || v > 2) return bad();
-    t.gemm = (int)v;
-    return IXH_OK;
-  case IXH_OPT_GEMM_TILE:
-    if (v < 0 || v > 2) return bad();
-    t.gemm_tile = (int)v;
-    return IXH_OK;
-  default: break;
-  }
-  if (!model_opts) return fail(IXH_EINVAL, "linalg: option %d does not apply to a PackedB8", option);
-  switch (option) {
-  case IXH_OPT_PARTS:
-    if (v < 0 || v > 4) return bad();
-    t.parts = (int)v;
-    return IXH_OK;
-  case IXH_OPT_PASS_TOKENS:
-    if (v < 1 || v > kMaxPassTokensOpt) return bad();
-    t.pass_tokens = (int)v;
-    return IXH_OK;
-  case IXH_OPT_QKV_FUSED:
-    if (v != 0 && v != 1) return bad();
-    t.qkv_fused = (int)v;
-    return IXH_OK;
-  case IXH_OPT_QKV_HEADS:
-    if (v != 1 && v != 2) return bad();
-    t.qkv_heads = (int)v;
-    return IXH_OK;
-  case IXH_OPT_LN_SEG:
-    if (v != 0 && v != 1) return bad();
-    t.ln_seg = (int)v;
-    return IXH_OK;
-  case IXH_OPT_FUSE_RES:
-    if (v < 0 || v > 4) return bad();
-    t.fuse_res = (int)v;
-    return IXH_OK;
-  case IXH_OPT_FUSE_MLP:
-    if (v < 0 || v > 2) return bad();
-    t.fuse_mlp = (int)v;
-    return IXH_OK;
-  case IXH_OPT_QKV_KBLOCK:
-    if (v != 0 && v != 1) return bad();
-    t.qkv_kblock = (int)v;
-    return IXH_OK;
-  default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
-  }
-}
-
-int get_tuning(const Tuning &t, int option, int64_t *v) {
-  switch (option) {
-  case IXH_OPT_PARTS: *v = t.parts; return IXH_OK;
-  case IXH_OPT_PASS_TOKENS: *v = t.pass_tokens; return IXH_OK;
-  case IXH_OPT_QKV_FUSED: *v = t.qkv_fused; return IXH_OK;
-  case IXH_OPT_QKV_HEADS: *v = t.qkv_heads; return IXH_OK;
-  case IXH_OPT_GEMM: *v = t.gemm; return IXH_OK;
-  case IXH_OPT_GEMM_TILE: *v = t.gemm_tile; return IXH_OK;
-  case IXH_OPT_LN_SEG: *v = t.ln_seg; return IXH_OK;
-  case IXH_OPT_FUSE_RES: *v = t.fuse_res; return IXH_OK;
-  case IXH_OPT_FUSE_MLP: *v = t.fuse_mlp; return IXH_OK;
-  case IXH_OPT_QKV_KBLOCK: *v = t.qkv_kblock; return IXH_OK;
-  default: return fail(IXH_EINVAL, "indecis: unknown option %d", option);
-  }
-}
 
 int validate_config(const ixh_config &c) {
   if (c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.intermediate <= 0 || c.vocab <= 0)
@@ -476,14 +377,7 @@ int rope_for(ixh_model *m, int global, int rows, const float **c, const float **
 }
 
 Workspace *acquire(ixh_model *m) {
-  {
-    std::lock_guard<std::mutex> lk(m->pool_mu);
-    if (!m->pool.empty()) {
-      Workspace *w = m->pool.back();
-      m->pool.pop_back();
-      return w;
-    }
-  }
+  if (Workspace *w = m->pool.take()) return w;
   Workspace *w = new Workspace();
   if (hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking) != hipSuccess) {
     delete w;
@@ -493,8 +387,7 @@ Workspace *acquire(ixh_model *m) {
 }
 
 void release(ixh_model *m, Workspace *w) {
-  std::lock_guard<std::mutex> lk(m->pool_mu);
-  m->pool.push_back(w);
+  m->pool.put(w);
 }
 
 struct WsGuard {
@@ -1060,7 +953,6 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
 
 // Token count from which a batch is split over several streams.
 constexpr int kSplitTokens = 4096;
-constexpr int kMaxPassTokens = kMaxPassTokensOpt;
 
 // The batch as P parts of about equal token counts, each on its own stream
 // (the caller's, then those of extra workspaces), issued back to back: the
@@ -1077,13 +969,8 @@ int forward_split(ixh_model *m, const Tuning &tune, const HeadSet *hs, Workspace
   if (P < 2 || N < kSplitTokens) return forward(m, tune, hs, w, st, d_ids, offs, B, out);
   // part p covers sequences [cut[p], cut[p+1]): the first starting at or
   // past p*N/P
-  std::vector<int> cut(P + 1, B);
-  cut[0] = 0;
-  for (int p = 1; p < P; p++) {
-    int b = cut[p - 1];
-    while (b < B && (int64_t)P * offs[b] < (int64_t)p * N) b++;
-    cut[p] = std::max(b, cut[p - 1]);
-  }
+  std::vector<int> cut;
+  split_points(offs, B, P, cut);
   const int H = m->cfg.hidden;
   for (int k = 0; k < nextra; k++)
     for (int e = 0; e < 2; e++)
@@ -1106,7 +993,7 @@ int forward_split(ixh_model *m, const Tuning &tune, const HeadSet *hs, Workspace
     offp[p].resize(b1 - b0 + 1);
     for (int b = b0; b <= b1; b++) offp[p][b - b0] = offs[b] - offs[b0];
     const int r = forward(m, tune, hs, wp, sp, d_ids + offs[b0], offp[p].data(), b1 - b0,
-                          out.at(b0, offs[b0], H, hs), &pend[p]);
+                          out.at(b0, offs[b0], H, hs->rp, hs->rt), &pend[p]);
     if (r && !rc) rc = r;
   }
   // st waits for every part whatever happened, so nothing is left queued
@@ -1138,36 +1025,10 @@ struct ExtraWs {
   }
 };
 
-int check_offs(const int32_t *offs, int B) {
-  if (B < 0 || (B > 0 && !offs)) return fail(IXH_EINVAL, "modernbert: inconsistent batch");
-  if (B == 0) return IXH_OK;
-  if (offs[0] != 0) return fail(IXH_EINVAL, "modernbert: inconsistent batch");
-  for (int b = 0; b < B; b++)
-    if (offs[b + 1] < offs[b]) return fail(IXH_EINVAL, "modernbert: inconsistent batch");
-  return IXH_OK;
-}
-
 // The handle's tuning, copied once per call.
 Tuning tuning_of(ixh_model *m) {
   std::lock_guard<std::mutex> lk(m->tune_mu);
   return m->tuning;
-}
-
-// Passes of whole sequences, in order, of at most t.pass_tokens tokens
-// each (a longer sequence takes a pass of its own): cut[i] .. cut[i+1].
-// Rows do not depend on their batch (TestMatMul8RowsIndependent), so the
-// results are those of one pass.
-int plan_passes(const Tuning &t, const int32_t *offs, int B, std::vector<int> &cut) {
-  cut.assign(1, 0);
-  for (int b = 0; b < B; b++) {
-    const int n = offs[b + 1] - offs[b];
-    if (n > kMaxPassTokens)
-      return fail(IXH_EINVAL, "modernbert: hip: sequence of %d tokens over the %d-token limit of a pass", n,
-                  kMaxPassTokens);
-    if (b > cut.back() && offs[b + 1] - offs[cut.back()] > t.pass_tokens) cut.push_back(b);
-  }
-  cut.push_back(B);
-  return IXH_OK;
 }
 
 // The heads the call needs (an error when out asks for logits and none
@@ -1209,7 +1070,7 @@ int encode_host(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, co
   if ((rc = weights_ready(m))) return rc;
   const Tuning tune = tuning_of(m);
   std::vector<int> cut;
-  if ((rc = plan_passes(tune, offs, B, cut))) return rc;
+  if ((rc = plan_passes(tune, m->cfg.hidden, m->cfg.intermediate, offs, B, cut))) return rc;
   WsGuard wg{m, acquire(m)};
   Workspace *w = wg.w;
   if (!w) return fail(IXH_EHIP, "modernbert: hip: stream creation failed");
@@ -1249,7 +1110,7 @@ int encode_host(ixh_model *m, const int32_t *ids, const int32_t *offs, int B, co
     if ((rc = forward_split(m, tune, hs, w, ex.ws.data(), (int)ex.ws.size(), st, w->ids.as<int32_t>(),
                             offp.data(), b1 - b0, dev)))
       return rc;
-    const Outputs h = out.at(b0, t0, H, hs);
+    const Outputs h = out.at(b0, t0, H, hs->rp, hs->rt);
     if (dev.states) HIPCK(hipMemcpyAsync(h.states, dev.states, 4 * (size_t)n * H, hipMemcpyDeviceToHost, st));
     if (dev.pooled)
       HIPCK(hipMemcpyAsync(h.pooled, dev.pooled, 4 * (size_t)(b1 - b0) * H, hipMemcpyDeviceToHost, st));
@@ -1272,20 +1133,38 @@ constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
 static __device__ __align__(256) int8_t scratch[kNoAllocScratchBytes];
 
 namespace {
+// Per device ordinal: the scratch copy's address, and the event each call
+// records after its work so that the next call's work waits for it; `order`
+// keeps a call's wait, launches and record together against other threads.
+struct NoAllocDev {
+  std::mutex order;
+  void *ptr = nullptr;
+  hipEvent_t done = nullptr;
+};
 std::mutex g_scratch_mu;
-void *g_scratch_ptr[64];  // per device ordinal
+NoAllocDev g_noalloc[64];
 
-int scratch_ptr(int dev, void **out) {
+// With dev current: resolves the device's scratch copy and creates its
+// event on first use (set-up; the entry point itself then allocates nothing).
+int scratch_ptr(int dev, NoAllocDev **out) {
   if (dev < 0 || dev >= 64) return fail(IXH_EINVAL, "linalg: hip: device %d", dev);
   std::lock_guard<std::mutex> lk(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  NoAllocDev &d = g_noalloc[dev];
+  if (!d.ptr) {
     void *p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return fail(IXH_EHIP, "linalg: hip: %s (hipGetSymbolAddress scratch)", hipGetErrorString(e));
-    g_scratch_ptr[dev] = p;
+    hipEvent_t ev = nullptr;
+    const hipError_t e2 = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e2 != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(IXH_EHIP, "linalg: hip: %s (scratch event)", hipGetErrorString(e2));
+    }
+    d.done = ev;
+    d.ptr = p;
   }
-  *out = g_scratch_ptr[dev];
+  *out = &d;
   return IXH_OK;
 }
 }  // namespace
@@ -1604,7 +1483,7 @@ int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs, i
   if (N > 0 && (rc = weights_ready(m))) return rc;
   const Tuning tune = tuning_of(m);
   std::vector<int> cut;
-  if ((rc = plan_passes(tune, offs, B, cut))) return rc;
+  if ((rc = plan_passes(tune, m->cfg.hidden, m->cfg.intermediate, offs, B, cut))) return rc;
   DEVGUARD(m->device);
   WsGuard wg{m, acquire(m)};
   Workspace *w = wg.w;
@@ -1639,7 +1518,7 @@ int ixh_encode_device(ixh_model *m, const int32_t *d_ids, const int32_t *offs, i
   std::vector<int32_t> offp;
   for (size_t i = 0; i + 1 < cut.size() && !rc; i++) {
     const int b0 = cut[i], b1 = cut[i + 1], t0 = offs[b0], n = offs[b1] - t0;
-    const Outputs o = out.at(b0, t0, H, &none);
+    const Outputs o = out.at(b0, t0, H, 0, 0);
     if (n == 0) {
       if (o.pooled) {
         launch_fill_u32(o.pooled, 0u, (size_t)(b1 - b0) * H, st);
@@ -1695,8 +1574,8 @@ int ixh_packb8_create(int device, const int8_t *q, const float *scale, int k, in
   if (layout != IXH_LAYOUT_ROWS && layout != IXH_LAYOUT_PANELS)
     return fail(IXH_EINVAL, "linalg: PackB8: layout %d", layout);
   DEVGUARD(device);
-  void *sp = nullptr;
-  int src = scratch_ptr(device, &sp);  // set-up: resolve the device's scratch copy now
+  NoAllocDev *nd = nullptr;
+  int src = scratch_ptr(device, &nd);  // set-up: resolve the device's scratch copy now
   if (src) return src;
   auto *b = new ixh_packed_b8();
   b->device = device;
@@ -1851,12 +1730,20 @@ int ixh_matmul8_noalloc(ixh_packed_b8 *b, float *d_c, int ldc, const float *d_a,
                 "scratch, over its %zu (at most %zu rows)",
                 m, M.kp, need, kNoAllocScratchBytes, (kNoAllocScratchBytes - 256) / (M.kp + 4));
   DEVGUARD(b->device);
-  void *sp = nullptr;
+  NoAllocDev *nd = nullptr;
   int rc;
-  if ((rc = scratch_ptr(b->device, &sp))) return rc;
-  int8_t *dq = (int8_t *)sp;
-  float *dsa = (float *)((char *)sp + qbytes);
+  if ((rc = scratch_ptr(b->device, &nd))) return rc;
+  int8_t *dq = (int8_t *)nd->ptr;
+  float *dsa = (float *)((char *)nd->ptr + qbytes);
   hipStream_t st = (hipStream_t)stream;
+  // calls on this GPU run one after another whatever their streams: this
+  // call's work waits for the previous call's event and records it after
+  // its own (a stream under graph capture takes neither: the graph orders it)
+  std::lock_guard<std::mutex> order(nd->order);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIPCK(hipStreamIsCapturing(st, &cap));
+  const bool serial = cap == hipStreamCaptureStatusNone;
+  if (serial) HIPCK(hipStreamWaitEvent(st, nd->done, 0));
   // quantizeA (int8.go:160-191) into the scratch: rows padded with zeros to Kp
   launch_quant_rows(d_a, lda, m, M.k, dq, M.kp, dsa, st);
   LAUNCHCK("quant_rows");
@@ -1878,6 +1765,7 @@ int ixh_matmul8_noalloc(ixh_packed_b8 *b, float *d_c, int ldc, const float *d_a,
   g.n_valid = M.n;
   run_gemm(accumulate ? EPI_ACCUM : EPI_STORE, g, pb_tuning(b), st);
   LAUNCHCK("matmul8");
+  if (serial) HIPCK(hipEventRecord(nd->done, st));
   return IXH_OK;
 }
 
@@ -2263,89 +2151,11 @@ int ixh_check_gelu(int device, int64_t bad[2]) {
 }  // extern "C"
 
 // ---- batching of concurrent requests ----------------------------------------
-// WithBatching / batcher (batch.go:1-82, model.go:136-160): worker threads
-// each take the first pending request and, without waiting, the requests
-// already queued while the batch stays under max_rows tokens, run them as
-// one encode pass (sequences end to end), and hand every request its
-// pooled rows; an error of the pass goes to every request of the batch.
-namespace {
-struct BatchReq {
-  const int32_t *ids;
-  const int32_t *offs;
-  int B, rows;
-  float *out;
-  int rc = IXH_OK;
-  std::string err;
-  bool done = false;
-};
-}  // namespace
-
+// WithBatching (model.go:136-160): the queue and its worker threads are
+// BatchQueue's; a worker's merged batch runs as one encode_host pass.
 struct ixh_batcher {
-  ixh_model *m = nullptr;
-  int max_rows = 0;
-  std::mutex mu;
-  std::condition_variable work_cv, done_cv;
-  std::deque<BatchReq *> queue;
-  bool stop = false;
-  int64_t batches = 0, requests = 0;
-  std::vector<std::thread> workers;
+  std::unique_ptr<BatchQueue> q;
 };
-
-namespace {
-// batcher.work (batch.go:51-82)
-void batcher_work(ixh_batcher *b) {
-  const int H = b->m->cfg.hidden;
-  std::vector<BatchReq *> batch;
-  std::vector<int32_t> ids, offs;
-  std::vector<float> pooled;
-  for (;;) {
-    batch.clear();
-    {
-      std::unique_lock<std::mutex> lk(b->mu);
-      b->work_cv.wait(lk, [&] { return b->stop || !b->queue.empty(); });
-      if (b->queue.empty()) return;  // closed and drained
-      batch.push_back(b->queue.front());
-      b->queue.pop_front();
-      int rows = batch[0]->rows;
-      while (rows < b->max_rows && !b->queue.empty()) {
-        batch.push_back(b->queue.front());
-        rows += b->queue.front()->rows;
-        b->queue.pop_front();
-      }
-    }
-    int B = 0;
-    for (BatchReq *r : batch) B += r->B;
-    offs.assign(B + 1, 0);
-    ids.clear();
-    int k = 0;
-    for (BatchReq *r : batch) {
-      ids.insert(ids.end(), r->ids, r->ids + r->offs[r->B]);
-      for (int s = 0; s < r->B; s++, k++) offs[k + 1] = offs[k] + (r->offs[s + 1] - r->offs[s]);
-    }
-    pooled.resize((size_t)B * H);
-    Outputs o;
-    o.pooled = pooled.data();
-    const int rc = encode_host(b->m, ids.data(), offs.data(), B, o);
-    size_t off = 0;
-    for (BatchReq *r : batch) {
-      if (rc) {
-        r->rc = rc;
-        r->err = g_err;
-      } else {
-        memcpy(r->out, pooled.data() + off, sizeof(float) * (size_t)r->B * H);
-      }
-      off += (size_t)r->B * H;
-    }
-    {
-      std::lock_guard<std::mutex> lk(b->mu);
-      for (BatchReq *r : batch) r->done = true;
-      b->batches++;
-      b->requests += (int64_t)batch.size();
-    }
-    b->done_cv.notify_all();
-  }
-}
-}  // namespace
 
 extern "C" {
 
@@ -2353,10 +2163,15 @@ int ixh_batcher_create(ixh_model *m, int workers, int max_rows, ixh_batcher **ou
   if (!m || !out) return fail(IXH_EINVAL, "modernbert: nil model");
   if (workers <= 0) workers = 2;
   if (max_rows <= 0) max_rows = 65536;
+  auto encode = [m](const int32_t *ids, const int32_t *offs, int B, float *pooled, std::string &err) {
+    Outputs o;
+    o.pooled = pooled;
+    const int rc = encode_host(m, ids, offs, B, o);
+    if (rc) err = g_err;
+    return rc;
+  };
   ixh_batcher *b = new ixh_batcher;
-  b->m = m;
-  b->max_rows = max_rows;
-  for (int i = 0; i < workers; i++) b->workers.emplace_back(batcher_work, b);
+  b->q.reset(new BatchQueue(m->cfg.hidden, workers, max_rows, encode));
   *out = b;
   return IXH_OK;
 }
@@ -2367,35 +2182,17 @@ int ixh_batcher_encode(ixh_batcher *b, const int32_t *ids, const int32_t *offs, 
   if ((rc = check_offs(offs, B))) return rc;
   if (B == 0) return IXH_OK;
   if ((offs[B] > 0 && !ids) || !out) return fail(IXH_EINVAL, "modernbert: inconsistent batch");
-  BatchReq r{ids, offs, B, offs[B], out};
-  {
-    std::unique_lock<std::mutex> lk(b->mu);
-    if (b->stop) return fail(IXH_EINVAL, "modernbert: batcher closed");
-    b->queue.push_back(&r);
-    b->work_cv.notify_one();
-    b->done_cv.wait(lk, [&] { return r.done; });
-  }
-  if (r.rc) return fail(r.rc, "%s", r.err.c_str());
+  std::string err;
+  if ((rc = b->q->submit(ids, offs, B, out, err))) return fail(rc, "%s", err.c_str());
   return IXH_OK;
 }
 
 int ixh_batcher_stats(ixh_batcher *b, int64_t *batches, int64_t *requests) {
   if (!b || !batches || !requests) return fail(IXH_EINVAL, "modernbert: nil batcher");
-  std::lock_guard<std::mutex> lk(b->mu);
-  *batches = b->batches;
-  *requests = b->requests;
+  b->q->counts(batches, requests);
   return IXH_OK;
 }
 
-void ixh_batcher_destroy(ixh_batcher *b) {
-  if (!b) return;
-  {
-    std::lock_guard<std::mutex> lk(b->mu);
-    b->stop = true;
-  }
-  b->work_cv.notify_all();
-  for (std::thread &t : b->workers) t.join();
-  delete b;
-}
+void ixh_batcher_destroy(ixh_batcher *b) { delete b; }
 
 }  // extern "C"

@@ -6,29 +6,13 @@
 
 #include <vector>
 
+#include "host_sched.h"
+
 struct ixh_model;   // include/indecis_hip.h
 struct ixh_config;
 struct ixh_tokenizer;
 
 namespace ixh {
-
-// Kernel choices of a model or PackedB8 handle (ixh_model_set_option,
-// ixh_packb8_set_option). Each call copies the handle's values once, so a
-// change never reaches a pass already running.
-struct Tuning {
-  int parts = 0;          // streams a large batch is split over: 0 auto, 1..4
-  int pass_tokens = 131072;  // most tokens of one encoder pass
-  int qkv_fused = 1;      // QKV GEMM fused with Attn8.Prepare (sequences <= 512 keys)
-  int qkv_heads = 1;      // heads a workgroup of the fused QKV kernel: 1 or 2
-  int gemm = 0;           // 0: gemm_as for Wi/stores, gemm_i8 residual; 1: gemm_i8 only;
-                          // 2: as 0 with the residual GEMMs on gemm_ws
-  int gemm_tile = 0;      // gemm_i8 tiles: 0 128x128/2 stages, 1 256x128/3, 2 128x128/3
-  int ln_seg = 1;         // LayerNorm lanes 8/16: 1 segment kernel, 0 whole-row LDS kernel
-  int fuse_res = 1;       // residual GEMMs fused with quantizeA of their input and the next LN
-  int fuse_mlp = 2;       // the MLP block (Wi, GeGLU, quantizeA, WoMLP, next LN) as one kernel:
-                          // 2 mlp_block (64 rows, transposed), 1 mlp_res (32 rows), 0 separate
-  int qkv_kblock = 1;     // the fused QKV kernel reads its input rows K-blocked (1) or row-major (0)
-};
 
 // Compute units of the current device (cached per device; 256 if the query
 // fails), for grids of resident workgroups.

@@ -1,5 +1,7 @@
 """The library's host-only C++ (tokenizer.cpp with its worker threads,
-safetensors.cpp fed truncated and corrupted files, embed.cpp) built with
+safetensors.cpp fed truncated and corrupted files, embed.cpp, and
+host_sched.cpp: options, pass planning, the workspace free list and the
+serving batcher's queue under concurrent clients) built with
 g++ under AddressSanitizer + UndefinedBehaviorSanitizer and under
 ThreadSanitizer, and run on the CPU by tests/sanitize/host_check.cpp (no
 GPU: the model entry points those files call are stubbed there)."""
@@ -11,7 +13,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "indecis_amd", "csrc")
-SOURCES = [os.path.join(CSRC, f) for f in ("tokenizer.cpp", "safetensors.cpp", "embed.cpp")]
+SOURCES = [os.path.join(CSRC, f) for f in ("tokenizer.cpp", "safetensors.cpp", "embed.cpp", "host_sched.cpp")]
 DRIVER = os.path.join(ROOT, "tests", "sanitize", "host_check.cpp")
 TOKENIZER = os.path.join(ROOT, "tests", "golden", "tokenizer", "tokenizer.json")
 SANITIZERS = {

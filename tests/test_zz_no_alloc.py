@@ -3,7 +3,9 @@ quantised activations go to the library's fixed per-GPU scratch) against
 ixh_matmul8 (MatMul8N, int8.go:89-155, on host buffers) bit for bit,
 through the C ABI: two calls in a row, the second with fewer rows (the
 scratch keeps the first call's contents), stored and accumulated, with row
-strides wider than the rows; sizes over the scratch are refused."""
+strides wider than the rows; calls issued on two streams without waiting in
+between (the library orders them on the device); sizes over the scratch
+are refused."""
 import ctypes as C
 
 import numpy as np
@@ -47,6 +49,36 @@ def test_matmul8_noalloc_equals_matmul8(k, n):
             got = dc.cpu().numpy()
             assert f32_bits_equal(got[:, :n], want), mismatch_report(got[:, :n], want)
             assert np.all(got[:, n:] == 3.5)  # past n: untouched
+    b.close()
+
+
+def test_matmul8_noalloc_two_streams():
+    """Calls on two streams, issued back to back, each bit-exact: the second
+    call's quantisation into the shared scratch waits for the first call's
+    GEMM."""
+    rng = np.random.default_rng(17)
+    k, n = 1152, 768
+    b = linalg.PackedB8(rng.integers(-127, 128, size=(n, k), dtype=np.int8),
+                        rng.uniform(1e-3, 1e-2, size=n).astype(np.float32))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]  # default priority
+    sizes = [4096, 2500, 4096, 1]
+    cases = []
+    for i, m in enumerate(sizes):
+        a = (rng.standard_normal((m, k)) * 2).astype(np.float32)
+        want = linalg.matmul8(np.zeros((m, n), np.float32), a, b, m)
+        cases.append((m, torch.from_numpy(a).cuda(), torch.zeros((m, n), dtype=torch.float32, device="cuda"),
+                      want))
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for _, _, dc, _ in cases:
+            dc.fill_(7.0)  # fill kernels on the current stream, finished before the calls
+        torch.cuda.synchronize()
+        for i, (m, da, dc, _) in enumerate(cases):
+            _call(b, dc, n, da, k, m, False, streams[i % 2].cuda_stream)
+        torch.cuda.synchronize()
+        for i, (m, da, dc, want) in enumerate(cases):
+            got = dc.cpu().numpy()
+            assert f32_bits_equal(got, want), f"rep {rep} call {i}: " + mismatch_report(got, want)
     b.close()
 
 
