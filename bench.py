@@ -184,9 +184,10 @@ def spans(np, model, cfg, seqs, args):
     9 logits a token, spanTagCount spans.go:125; logits spans.go:449-459)
     on every token of the batch, in the encoder pass (ixh_encode_heads:
     host ids in, host float64 logits out, mean pooling as infer pools with
-    Spans questions, spans.go:466-476). Reports the call's rate and the head
-    kernel's HBM rate from its HIP events (its algorithmic bytes: each
-    token's float32 state in, 9 float64 logits out, the weights once)."""
+    Spans questions, spans.go:466-476). Reports the call's rate (the
+    library's default split) and the head kernel's HBM rate from its HIP
+    events with the batch as one part (its algorithmic bytes: each token's
+    float32 state in, 9 float64 logits out, the weights once)."""
     from indecis_amd import heads as hd
     rng = np.random.default_rng(11)
     rows = hd.span_tag_count(4)
@@ -198,6 +199,10 @@ def spans(np, model, cfg, seqs, args):
     for _ in range(args.steps):
         model.encode_heads(seqs, mean=True, pooled=False)
     dt = (time.perf_counter() - t0) / args.steps
+    # the head kernel alone: the batch as one part, so that no kernel of
+    # another part shares the CUs while its launches are timed
+    model.set_option("parts", 1)
+    model.encode_heads(seqs, mean=True, pooled=False)
     model.set_profiling(True, only="head_tokens")
     for _ in range(args.steps):
         model.encode_heads(seqs, mean=True, pooled=False)

@@ -230,7 +230,7 @@ struct RopeTab {
 // pooled-row heads' weight rows end to end, then the per-token heads'.
 struct HeadSet {
   int rp = 0, rt = 0;     // rows of the pooled-row heads, of the per-token heads
-  DevBuf wp, bp, wt, bt;  // [rows][H] weights, [rows] biases
+  DevBuf wp, bp, wt, bt;  // [rows][H] weights widened to float64 (exact), [rows] float32 biases
 };
 
 struct Workspace {
@@ -940,10 +940,10 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
         launch_pool(xn, d_offs, B, H, c.pooling == IXH_POOL_CLS && !out.mean, pooled, st));
   if (out.zp && heads->rp > 0)
     RUN("head_pooled", 0, (double)B * (4 * dH + 8 * heads->rp),
-        launch_head_logits(pooled, B, H, heads->wp.as<float>(), heads->bp.as<float>(), heads->rp, out.zp, st));
+        launch_head_logits(pooled, B, H, heads->wp.as<double>(), heads->bp.as<float>(), heads->rp, out.zp, st));
   if (out.zt && heads->rt > 0 && N > 0)
     RUN("head_tokens", 0, dN * (4 * dH + 8 * heads->rt),
-        launch_head_logits(xn, N, H, heads->wt.as<float>(), heads->bt.as<float>(), heads->rt, out.zt, st));
+        launch_head_logits(xn, N, H, heads->wt.as<double>(), heads->bt.as<float>(), heads->rt, out.zt, st));
 #undef RUN
   if (defer) return prof.err;
   // tables used by queued work stay alive until the stream has run them
@@ -1375,10 +1375,12 @@ int ixh_model_set_heads(ixh_model *m, int n, const int *rows, const int *per_tok
     m->heads.reset();
     return IXH_OK;
   }
-  std::vector<float> wp, bp, wt, bt;
+  std::vector<double> wp, wt;
+  std::vector<float> bp, bt;
   for (int h = 0; h < n; h++) {
     if (rows[h] <= 0 || !w[h] || !b[h]) return fail(IXH_EINVAL, "indecis: head %d: bad arguments", h);
-    std::vector<float> &W = per_token[h] ? wt : wp, &Bv = per_token[h] ? bt : bp;
+    std::vector<double> &W = per_token[h] ? wt : wp;
+    std::vector<float> &Bv = per_token[h] ? bt : bp;
     W.insert(W.end(), w[h], w[h] + (size_t)rows[h] * H);
     Bv.insert(Bv.end(), b[h], b[h] + rows[h]);
   }
@@ -1387,15 +1389,15 @@ int ixh_model_set_heads(ixh_model *m, int n, const int *rows, const int *per_tok
   hs->rp = (int)bp.size();
   hs->rt = (int)bt.size();
   int rc;
-  if ((rc = hs->wp.ensure(4 * wp.size())) || (rc = hs->bp.ensure(4 * bp.size())) ||
-      (rc = hs->wt.ensure(4 * wt.size())) || (rc = hs->bt.ensure(4 * bt.size())))
+  if ((rc = hs->wp.ensure(8 * wp.size())) || (rc = hs->bp.ensure(4 * bp.size())) ||
+      (rc = hs->wt.ensure(8 * wt.size())) || (rc = hs->bt.ensure(4 * bt.size())))
     return rc;
   if (!wp.empty()) {
-    HIPCK(hipMemcpy(hs->wp.p, wp.data(), 4 * wp.size(), hipMemcpyHostToDevice));
+    HIPCK(hipMemcpy(hs->wp.p, wp.data(), 8 * wp.size(), hipMemcpyHostToDevice));
     HIPCK(hipMemcpy(hs->bp.p, bp.data(), 4 * bp.size(), hipMemcpyHostToDevice));
   }
   if (!wt.empty()) {
-    HIPCK(hipMemcpy(hs->wt.p, wt.data(), 4 * wt.size(), hipMemcpyHostToDevice));
+    HIPCK(hipMemcpy(hs->wt.p, wt.data(), 8 * wt.size(), hipMemcpyHostToDevice));
     HIPCK(hipMemcpy(hs->bt.p, bt.data(), 4 * bt.size(), hipMemcpyHostToDevice));
   }
   std::lock_guard<std::mutex> lk(m->heads_mu);
@@ -1553,13 +1555,14 @@ int ixh_head_logits(ixh_model *m, const float *x, int T, const float *w, const f
   DEVGUARD(m->device);
   DevBuf dx, dw, db, dz;
   int rc;
-  if ((rc = dx.ensure(4 * (size_t)T * H)) || (rc = dw.ensure(4 * (size_t)rows * H)) ||
+  if ((rc = dx.ensure(4 * (size_t)T * H)) || (rc = dw.ensure(8 * (size_t)rows * H)) ||
       (rc = db.ensure(4 * (size_t)rows)) || (rc = dz.ensure(8 * (size_t)T * rows)))
     return rc;
+  const std::vector<double> w64(w, w + (size_t)rows * H);  // widened: exact
   HIPCK(hipMemcpy(dx.p, x, 4 * (size_t)T * H, hipMemcpyHostToDevice));
-  HIPCK(hipMemcpy(dw.p, w, 4 * (size_t)rows * H, hipMemcpyHostToDevice));
+  HIPCK(hipMemcpy(dw.p, w64.data(), 8 * w64.size(), hipMemcpyHostToDevice));
   HIPCK(hipMemcpy(db.p, b, 4 * (size_t)rows, hipMemcpyHostToDevice));
-  launch_head_logits(dx.as<float>(), T, H, dw.as<float>(), db.as<float>(), rows, dz.as<double>(), 0);
+  launch_head_logits(dx.as<float>(), T, H, dw.as<double>(), db.as<float>(), rows, dz.as<double>(), 0);
   LAUNCHCK("head_logits");
   HIPCK(hipDeviceSynchronize());
   HIPCK(hipMemcpy(z, dz.p, 8 * (size_t)T * rows, hipMemcpyDeviceToHost));

@@ -230,7 +230,7 @@ void launch_pool(const float *xn, const int32_t *offs, int B, int H, int cls,
                  float *out, hipStream_t s);
 
 // head.logits (heads.go:63-74) over T rows.
-void launch_head_logits(const float *x, int T, int H, const float *w,
+void launch_head_logits(const float *x, int T, int H, const double *w,
                         const float *b, int rows, double *z, hipStream_t s);
 
 // ---- attention ------------------------------------------------------------

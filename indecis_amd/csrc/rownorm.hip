@@ -566,113 +566,150 @@ __global__ void pool_kernel(const float *xn, const int32_t *offs, int H, int cls
   *dst = (float)(acc / (double)n);
 }
 
-// heads.go:63-74: z = sum f64(w)*f64(x), in order, + f64(b).
 // head.logits (heads.go:63-74) and the spans head (spans.go:449-459):
 // z[t][r] = sum_i f64(w[r][i]) * f64(x[t][i]) in column order, + f64(b[r]).
 // Each product of two float32 is exact in float64, so fma(x, w, s) rounds
-// once where the reference's s + x*w does: the same bits. One workgroup of
-// 4 waves takes HL_T tokens (lane l: tokens l and l + 64) and up to rg <=
-// HL_R rows (wave w the rows r0 + w, r0 + w + 4, ...: at most 2 HL_R / 4
-// chains a thread, each weight read from LDS serving two of them;
-// more rows take more workgroups along y, each reading x again); the rows'
-// weights sit in LDS widened to float64 (every lane of a wave reads the
-// same one: a broadcast); x comes through LDS in chunks of HL_C columns,
-// loaded as whole 128-byte pieces of its rows (8 threads a token) HL_PD
-// chunks ahead.
-constexpr int HL_T = 128, HL_R = 12, HL_C = 32, HL_XLD = HL_C + 4, HL_PD = 2;
-constexpr int HL_WMAX = 16384;  // float64 weights a workgroup holds (rg * H <= HL_WMAX: 128 KB)
-constexpr int HL_RW = HL_R / 4;  // chains a thread a token
-static_assert(64 % (HL_PD * HL_C) == 0, "every width (a multiple of 64) is whole rounds of the ring");
-__global__ __launch_bounds__(256) void head_logits_kernel(const float *x, int T, int H, const float *w,
-                                                          const float *b, int rows, int rg, double *z) {
-  extern __shared__ __attribute__((aligned(16))) double hl_w[];  // [rg][H]
-  __shared__ __attribute__((aligned(16))) float xs[HL_T * HL_XLD];
-  typedef float v4f __attribute__((ext_vector_type(4)));  // (an array of HIP's float4 struct stays in memory)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int t0 = blockIdx.x * HL_T, r0 = blockIdx.y * rg;
+// once where the reference's s + x*w does: the same bits.
+//
+// One workgroup of NW waves takes 64 tokens (lane = token) and rg <= NW RW
+// rows: wave w the rows r0 + w + NW j, j < RW (a row past the workgroup's
+// last is computed on its last row and not stored). x arrives in stages of
+// 32 columns (8 KB: 64 tokens x 128 bytes) by direct-to-LDS buffer loads,
+// HT_S stages in a ring, HT_S - 1 in flight; slot j of token t holds the
+// token's 16-byte piece j ^ ((t >> 1) & 7), so the lanes' 16-byte reads of
+// one piece fall in distinct banks. Every lane uses the same weight at a
+// time, so the weights (widened to float64, exact) stay out of LDS: a
+// stage's 32 weights of a row are two float64 registers whose lane l holds
+// column 16 h + l % 16, loaded with the stage's x, and each FMA takes its
+// weight by DPP row_newbcast (lane n of every 16-lane row, to the row) —
+// no broadcast read from LDS (LDS returns 128 bytes a clock: a float64 to
+// 64 lanes would cost 4 clocks an FMA) and no scalar loads (whose waits,
+// one for all in flight, left the kernel at half the rate). Stages past
+// the last load the last one again (the count of loads in flight stays
+// fixed; nothing reads them). The ring is read by lds_read16: the
+// compiler, seeing an LDS read, would wait for every direct-to-LDS load in
+// flight first.
+constexpr int HT_T = 64, HT_C = 32, HT_S = 4;
+constexpr int HT_STAGE = HT_T * HT_C * 4;  // bytes a stage
+typedef float hv4 __attribute__((ext_vector_type(4)));
+// 16 bytes from LDS, outside the compiler's view (no wait is inserted for
+// it or for loads in flight); lgkm_wait makes its results usable
+__device__ __forceinline__ hv4 lds_read16(uint32_t addr) {
+  hv4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ void lgkm_wait(hv4 (&v)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+}
+// acc[j] += bcast_N(w[j]) * x for the RW rows j: v_fmac_f64 with the
+// weight register as the DPP source (row_newbcast:N). The s_nop keeps two
+// wait states between any VALU write of a weight register and its DPP
+// read (the hardware's rule for DPP sources; the weights come from loads,
+// but the compiler may copy them); one statement for the rows keeps the
+// compiler from placing anything between the nop and the FMAs.
+#define HT_FMA(A, W) "v_fmac_f64_dpp %" #A ", %" #W ", %[x] row_newbcast:%[n] row_mask:0xf bank_mask:0xf"
+template <int N, int RW>
+__device__ __forceinline__ void fmac_bc(double (&acc)[RW], const double (&w)[RW], double x) {
+  if constexpr (RW == 1)
+    asm volatile("s_nop 1\n\t" HT_FMA(0, 1) : "+v"(acc[0]) : "v"(w[0]), [x] "v"(x), [n] "i"(N));
+  else if constexpr (RW == 2)
+    asm volatile("s_nop 1\n\t" HT_FMA(0, 2) "\n\t" HT_FMA(1, 3)
+                 : "+v"(acc[0]), "+v"(acc[1])
+                 : "v"(w[0]), "v"(w[1]), [x] "v"(x), [n] "i"(N));
+  else
+    asm volatile("s_nop 1\n\t" HT_FMA(0, 3) "\n\t" HT_FMA(1, 4) "\n\t" HT_FMA(2, 5)
+                 : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2])
+                 : "v"(w[0]), "v"(w[1]), "v"(w[2]), [x] "v"(x), [n] "i"(N));
+}
+#undef HT_FMA
+template <int RW, int NW>
+__global__ __launch_bounds__(64 * NW) void head_logits_kernel(const float *__restrict__ x, int T, int H,
+                                                              const double *__restrict__ w,
+                                                              const float *__restrict__ b, int rows, int rg,
+                                                              double *__restrict__ z) {
+  __shared__ __attribute__((aligned(16))) float hx[HT_S * HT_T * HT_C];
+  // a stage is 8 wave-wide loads (1 KB each); wave w issues loads
+  // LPT w .. LPT w + LPT - 1, the ones past 7 repeating load 7 (the same
+  // bytes to the same place), so every wave runs the same code
+  constexpr int LPT = (HT_STAGE / 1024 + NW - 1) / NW;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t0 = blockIdx.x * HT_T, r0 = blockIdx.y * rg;
   const int nr = min(rg, rows - r0);
-  const int nt = min(HL_T, T - t0);
-  // the weights, float4 a thread a round, every load issued before the
-  // first conversion; rounds past the rows' end repeat the last float4
-  // (the same values to the same place: no branch)
-  {
-    constexpr int WR = HL_WMAX / 4 / 256;  // rounds at the largest rg * H
-    const int n4 = nr * H / 4;
-    v4f wv[WR];
-    sfor<WR>([&](auto kv) { wv[kv.value] = *(const v4f *)(w + (size_t)r0 * H + 4 * min(tid + 256 * kv.value, n4 - 1)); });
-    sfor<WR>([&](auto kv) {
-      const int i = min(tid + 256 * kv.value, n4 - 1);
-      *(double2 *)(hl_w + 4 * i) = make_double2((double)wv[kv.value].x, (double)wv[kv.value].y);
-      *(double2 *)(hl_w + 4 * i + 2) = make_double2((double)wv[kv.value].z, (double)wv[kv.value].w);
-    });
-  }
-  // chunk loads: piece p = tid + 256 k of the chunk's HL_T x HL_C floats,
-  // token p / 8, float4 p % 8 (tokens past T read token T-1, unused); past
-  // the last chunk the loads read the last one again (unused)
-  constexpr int PPT = HL_T * HL_C / 4 / 256;  // float4 pieces a thread
-  v4f nx[HL_PD][PPT];
-  const float *xp[PPT];
-  sfor<PPT>([&](auto kv) {
-    const int p = tid + 256 * kv.value;
-    xp[kv.value] = x + (size_t)(t0 + min(p / 8, nt - 1)) * H + 4 * (p % 8);
+  const int nt = min(HT_T, T - t0);
+  const int ns = H / HT_C;
+  // load k of this wave: slot s = 64 q + lane of a stage (q its 1 KB
+  // piece), token s / 8, global piece (s % 8) ^ ((token >> 1) & 7); through
+  // a buffer descriptor over the workgroup's tokens (tokens past T read 0,
+  // never stored), the lane's offset fixed in a VGPR and the stage's
+  // column in the SGPR offset
+  const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x + (size_t)t0 * H, (uint32_t)(nt * H * 4));
+  uint32_t voff[LPT];
+  int dst[LPT];
+  sfor<LPT>([&](auto kv) {
+    const int q = min(LPT * wave + kv.value, HT_STAGE / 1024 - 1);
+    const int s = 64 * q + lane, t = s >> 3;
+    voff[kv.value] = (uint32_t)(t * H + 4 * ((s & 7) ^ ((t >> 1) & 7))) * 4u;
+    dst[kv.value] = 256 * q;
   });
-  auto load = [&](int c0, auto uv) {
-    sfor<PPT>([&](auto kv) { nx[uv.value][kv.value] = *(const v4f *)(xp[kv.value] + min(c0, H - HL_C)); });
+  const double *wl[RW];  // this lane's weights: row j, column lane % 16
+#pragma unroll
+  for (int j = 0; j < RW; j++) wl[j] = w + (size_t)(r0 + min(wave + NW * j, nr - 1)) * H + (lane & 15);
+  double wq[HT_S][2][RW];  // the ring's weights: stage slot, 16-column half, row
+  auto issue = [&](auto uv, int c) {
+    constexpr int u = decltype(uv)::value % HT_S;
+    const int cc = HT_C * min(c, ns - 1);
+    const uint32_t soff = 4u * (uint32_t)cc;
+    sfor<LPT>([&](auto kv) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(hx + u * (HT_T * HT_C) + dst[kv.value]), 16,
+                                               voff[kv.value], soff, 0, 0);
+    });
+#pragma unroll
+    for (int j = 0; j < RW; j++) {
+      wq[u][0][j] = wl[j][cc];
+      wq[u][1][j] = wl[j][cc + 16];
+    }
   };
-  // chains: tokens lane and lane + 64, rows wave + 4j (a row past nr is
-  // computed on row nr - 1 and not stored: no branch in the loop)
-  double acc[2][HL_RW];
-  int roff[HL_RW];
+  double acc[RW];
 #pragma unroll
-  for (int j = 0; j < HL_RW; j++) {
-    acc[0][j] = acc[1][j] = 0.0;
-    roff[j] = min(wave + 4 * j, nr - 1) * H;
-  }
-  sfor<HL_PD>([&](auto uv) { load(HL_C * uv.value, uv); });
-  auto chunk = [&](int cb, auto uv) {
-      constexpr int u = decltype(uv)::value;
-      const int c0 = cb + HL_C * u;
-
-      __syncthreads();  // the previous chunk is read (and, first, the weights are in)
-      sfor<PPT>([&](auto kv) {
-        const int p = tid + 256 * kv.value;
-        *(v4f *)(xs + (p / 8) * HL_XLD + 4 * (p % 8)) = nx[u][kv.value];
-      });
-      load(c0 + HL_PD * HL_C, uv);
-      __syncthreads();
+  for (int j = 0; j < RW; j++) acc[j] = 0.0;
+  const uint32_t xl = (uint32_t)(size_t)(lds_ptr)hx + 128u * lane;  // this lane's token row, slot 0
+  const int sw = (lane >> 1) & 7;
+  // stage c from ring slot u: 2 + RW loads a thread in flight for each
+  // later stage (LPT x pieces, 2 RW weights)
+  auto stage = [&](int c, auto uv) {
+    constexpr int u = decltype(uv)::value;
+    wait_vmcnt<(LPT + 2 * RW) * (HT_S - 2)>();  // this thread's loads of stage c have landed
+    lds_barrier();                              // everyone's are, and stage c - 1 is read
+    issue(std::integral_constant<int, u + HT_S - 1>{}, c + HT_S - 1);
+    const uint32_t st = xl + (uint32_t)(u * HT_STAGE);
+    hv4 v[8];
 #pragma unroll
-      for (int i = 0; i < HL_C; i += 4) {
-        double xd[2][4];
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const float4 v = *(const float4 *)(xs + (lane + 64 * h) * HL_XLD + i);
-          xd[h][0] = (double)v.x;
-          xd[h][1] = (double)v.y;
-          xd[h][2] = (double)v.z;
-          xd[h][3] = (double)v.w;
-        }
-#pragma unroll
-        for (int j = 0; j < HL_RW; j++) {
-          const double *wr = hl_w + roff[j] + c0 + i;
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const double wv = wr[e];
-            acc[0][j] = __builtin_fma(xd[0][e], wv, acc[0][j]);
-            acc[1][j] = __builtin_fma(xd[1][e], wv, acc[1][j]);
-          }
-        }
-      }
+    for (int i = 0; i < 8; i++) v[i] = lds_read16(st + 16u * (uint32_t)(i ^ sw));
+    lgkm_wait(v);
+    sfor<8>([&](auto iv) {
+      constexpr int i = decltype(iv)::value, h = i / 4, n0 = 4 * (i % 4);
+      const double xd[4] = {(double)v[i].x, (double)v[i].y, (double)v[i].z, (double)v[i].w};
+      fmac_bc<n0>(acc, wq[u][h], xd[0]);
+      fmac_bc<n0 + 1>(acc, wq[u][h], xd[1]);
+      fmac_bc<n0 + 2>(acc, wq[u][h], xd[2]);
+      fmac_bc<n0 + 3>(acc, wq[u][h], xd[3]);
+    });
   };
-  for (int cb = 0; cb < H; cb += HL_PD * HL_C) sfor<HL_PD>([&](auto uv) { chunk(cb, uv); });
+  sfor<HT_S - 1>([&](auto kv) { issue(kv, kv.value); });
+  // whole rounds of the ring, then the stages left
+  int cb = 0;
+  for (; cb + HT_S <= ns; cb += HT_S) sfor<HT_S>([&](auto uv) { stage(cb + uv.value, uv); });
+  sfor<HT_S - 1>([&](auto uv) {
+    if (cb + uv.value < ns) stage(cb + uv.value, uv);
+  });
+  wait_vmcnt<0>();  // the repeated loads past the last stage land before the workgroup ends
+  if (lane < nt) {
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
-    const int tk = lane + 64 * h;
-    if (tk < nt) {
-#pragma unroll
-      for (int j = 0; j < HL_RW; j++) {
-        const int r = wave + 4 * j;
-        if (r < nr) z[(size_t)(t0 + tk) * rows + r0 + r] = acc[h][j] + (double)b[r0 + r];
-      }
+    for (int j = 0; j < RW; j++) {
+      const int r = wave + NW * j;
+      if (r < nr) z[(size_t)(t0 + lane) * rows + r0 + r] = acc[j] + (double)b[r0 + r];
     }
   }
 }
@@ -767,22 +804,42 @@ void launch_pool(const float *xn, const int32_t *offs, int B, int H, int cls, fl
   pool_kernel<<<grid, 256, 0, s>>>(xn, offs, H, cls, out);
 }
 
-void launch_head_logits(const float *x, int T, int H, const float *w, const float *b, int rows,
+void launch_head_logits(const float *x, int T, int H, const double *w, const float *b, int rows,
                         double *z, hipStream_t s) {
   if (T <= 0 || rows <= 0) return;
-  // rows a workgroup: up to HL_R whose float64 weights fit in the dynamic
-  // LDS (H a multiple of HL_C: the model's width is one of 64); fewer rows,
-  // less LDS, more workgroups a CU
-  constexpr int kMaxDyn = HL_WMAX * sizeof(double);
-  const int rg = std::max(1, std::min(std::min(HL_R, rows), HL_WMAX / H));
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute((const void *)head_logits_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDyn);
-    attr = true;
+  // up to 12 rows a workgroup: NW (2-4) waves of RW (1-3) rows, NW chosen
+  // for the fewest chains computed (the larger NW on a tie); more rows take
+  // more workgroups along y, each reading x again
+  int nw = 4, rw = 3;
+  if (rows < 12) {
+    int best = 1 << 30;
+    for (int n = 2; n <= 4; n++) {
+      const int r = (rows + n - 1) / n;
+      if (r <= 3 && n * r <= best) best = n * r, nw = n, rw = r;
+    }
   }
-  const dim3 grid((unsigned)((T + HL_T - 1) / HL_T), (unsigned)((rows + rg - 1) / rg));
-  const size_t shm = (size_t)rg * H * sizeof(double);
-  head_logits_kernel<<<grid, 256, shm, s>>>(x, T, H, w, b, rows, rg, z);
+  const int rg = std::min(rows, nw * rw);
+  const dim3 grid((unsigned)((T + HT_T - 1) / HT_T), (unsigned)((rows + rg - 1) / rg));
+  auto go = [&](auto rwc, auto nwc) {
+    head_logits_kernel<decltype(rwc)::value, decltype(nwc)::value>
+        <<<grid, 64 * decltype(nwc)::value, 0, s>>>(x, T, H, w, b, rows, rg, z);
+  };
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  using I4 = std::integral_constant<int, 4>;
+  auto by_rw = [&](auto nwc) {
+    switch (rw) {
+      case 1: go(I1{}, nwc); break;
+      case 2: go(I2{}, nwc); break;
+      default: go(I3{}, nwc); break;
+    }
+  };
+  switch (nw) {
+    case 2: by_rw(I2{}); break;
+    case 3: by_rw(I3{}); break;
+    default: by_rw(I4{}); break;
+  }
 }
 
 }  // namespace ixh

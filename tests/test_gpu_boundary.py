@@ -228,12 +228,14 @@ def test_heads_on_device(pooling, mean):
 def test_head_logits_kernel_shapes(hidden):
     """head.logits (heads.go:63-74) on the device (ixh_head_logits): the
     float64 sums in column order for row counts within and past one
-    workgroup's 12 rows, token counts around its 64 tokens, and rows with
-    large, tiny and cancelling values, equal the oracle's bit for bit."""
+    workgroup's 12 rows (every shape of 2-4 waves of 1-3 rows), token
+    counts around its 64 tokens, and rows with large, tiny and cancelling
+    values, equal the oracle's bit for bit."""
     cfg = small_cfg(layers=1) if hidden == 256 else base_cfg(layers=1)
     w, gpu, _ = _pair(cfg, seed=48)
     rng = np.random.default_rng(48)
-    for T, rows in ((1, 1), (63, 9), (64, 12), (65, 13), (1000, 30), (130, 4)):
+    for T, rows in ((1, 1), (63, 9), (64, 12), (65, 13), (1000, 30), (130, 4), (129, 2), (200, 3), (70, 5),
+                    (257, 7), (4099, 9)):
         x = rng.standard_normal((T, hidden)).astype(np.float32)
         x[0, :8] = [3e38, -3e38, 1e-38, -1e-38, 1.0, -1.0, 65504.0, 1e-7]
         hw = (rng.standard_normal((rows, hidden)) * 0.02).astype(np.float32)
