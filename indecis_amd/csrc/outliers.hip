@@ -6,8 +6,9 @@
 //  * the chosen input channels zeroed in a copy of A before quantizeA;
 //  * after the GEMM, per output element, the chosen channels' products
 //    a[i][j] * f32(q[col][j] * sb[col]) added one by one in the chosen
-//    order (product and sum rounded separately, as gc on amd64 computes
-//    ci[col] += x * wv), then the bias (AddTo, vec_scalar.go:97-101).
+//    order (product and sum rounded separately, as gc computes
+//    ci[col] += x * wv for amd64 at GOAMD64 v1/v2, which has no scalar
+//    FMA), then the bias (AddTo, vec_scalar.go:97-101).
 // The channel choice itself (a float32 mean in channel order, a partial
 // selection of the 32 largest) runs on the host over the k maxima.
 #include "ixh_device.h"

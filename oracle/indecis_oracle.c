@@ -387,6 +387,23 @@ float ixo_exp_shift(float *x, int n, float m, int lanes) {
   return sum;
 }
 
+/* linalg/vec_simd.go:64-91: the vector body rounds x*inv (a product, then
+ * the magic-number add and subtract, each rounded) V values at a time and
+ * sums them in int32 lanes; the tail rounds roundHalfEven(x*inv) — the same
+ * operations, so with no fused multiply-add in the tail every element has
+ * the same formula (vec_scalar.go:23-31 for lanes == 0). The int32 sum is
+ * exact in any order (at most 255 n). */
+int32_t ixo_quantize_row_u8(uint8_t *dst, const float *x, int n, float inv, int lanes) {
+  (void)lanes;
+  int32_t sum = 0;
+  for (int i = 0; i < n; i++) {
+    const int32_t q = (int32_t)ixo_round_half_even(x[i] * inv);
+    dst[i] = (uint8_t)q;
+    sum += q;
+  }
+  return sum;
+}
+
 /* internal/modernbert/model.go:266-274. */
 void ixo_rope_table(double theta, int D, int rows, float *cos_t, float *sin_t) {
   int half = D / 2;

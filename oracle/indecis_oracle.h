@@ -11,8 +11,14 @@
  * Every function restates one reference function, cited file:line, with
  * the same float32/float64 operations in the same order: explicit fmaf()
  * where the reference fuses (Go SIMD MulAdd, VFMADD), separate roundings
- * where it does not (gc on amd64 never contracts scalar code). Build with
- * -ffp-contract=off and without -ffast-math.
+ * where it does not. Scalar Go code is taken to be unfused: the reference
+ * is built at GOAMD64 v1 or v2 (Go's default is v1), where the compiler
+ * has no FMA instruction for scalar float code. The Go specification lets
+ * an implementation fuse x*y + z, and from GOAMD64 v3 the instruction is
+ * there: a v3 build may round exp32, roundHalfEven(x*inv) in quantizeA's
+ * and QuantizeRowU8's scalar tails, and the scalar LayerNorm's d*d sum
+ * differently (tests/golden/go_semantics.json holds vectors that tell).
+ * Build with -ffp-contract=off and without -ffast-math.
  *
  * `lanes` is the Go simd vector length V of the reference host: 0 for a
  * build without GOEXPERIMENT=simd (vec_scalar.go), 4 (SSE/Neon), 8 (AVX2)
@@ -96,6 +102,10 @@ void ixo_gelu_mul(float *o, const float *a, const float *b, int n, int lanes);
 
 /* ExpShift (linalg/vec_simd.go:220-264; lanes==0: vec_scalar.go:50-58). */
 float ixo_exp_shift(float *x, int n, float m, int lanes);
+
+/* QuantizeRowU8 (linalg/vec_simd.go:64-91; lanes==0: vec_scalar.go:23-31):
+ * dst[i] = uint8(RNE(x[i]*inv)), the sum of the rounded values. */
+int32_t ixo_quantize_row_u8(uint8_t *dst, const float *x, int n, float inv, int lanes);
 
 /* ropeFor (internal/modernbert/model.go:256-277): cos/sin [rows][D/2]. */
 void ixo_rope_table(double theta, int D, int rows, float *cos_t, float *sin_t);

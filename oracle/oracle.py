@@ -78,6 +78,8 @@ def lib():
         L.ixo_gelu_mul.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int]
         L.ixo_exp_shift.argtypes = [f32p, C.c_int, C.c_float, C.c_int]
         L.ixo_exp_shift.restype = C.c_float
+        L.ixo_quantize_row_u8.argtypes = [C.POINTER(C.c_uint8), f32p, C.c_int, C.c_float, C.c_int]
+        L.ixo_quantize_row_u8.restype = C.c_int32
         L.ixo_rope_table.argtypes = [C.c_double, C.c_int, C.c_int, f32p, f32p]
         L.ixo_rope.argtypes = [f32p, f32p, f32p, C.c_int]
         L.ixo_attend8.argtypes = [f32p, C.c_int, f32p, f32p, f32p, C.c_int, C.c_int,
@@ -247,6 +249,13 @@ def exp_shift(x, m, lanes=8):
     x = _c(x, np.float32).copy()
     s = lib().ixo_exp_shift(x, x.size, float(m), lanes)
     return x, s
+
+
+def quantize_row_u8(x, inv, lanes=8):
+    x = _c(x, np.float32)
+    dst = np.zeros(x.size, np.uint8)
+    s = lib().ixo_quantize_row_u8(dst.ctypes.data_as(C.POINTER(C.c_uint8)), x, x.size, float(inv), lanes)
+    return dst, int(s)
 
 
 def rope_table(theta, D, rows):

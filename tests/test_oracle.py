@@ -768,3 +768,40 @@ def test_vnni_gemm_equals_restatement():
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     finally:
         orc.set_gemm(0)
+
+
+# ---- the vectors a Go build compares against --------------------------------
+
+def test_go_semantics_vectors():
+    """tests/golden/go_semantics.json (written by make_go_vectors.py): the
+    oracle still gives, bit for bit, the LayerNormRow, ExpShift,
+    QuantizeRowU8 and GeluMul outputs that a maintainer compares the Go
+    reference against, for every lane width; and each
+    crafted QuantizeRowU8 tie is one where a fused x*inv + magic (RNE of the
+    exact product, computed here in float64) rounds the other way, so the
+    vectors tell a build that fuses the tail."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "go_semantics.json")
+    doc = json.load(open(path))
+    f32 = lambda v: np.array(v, np.uint32).view(np.float32)
+    for c in doc["layernorm"]:
+        o = orc.layernorm_rows(f32(c["x"])[None, :], f32(c["gamma"]), eps=c["eps"], lanes=c["lanes"])[0]
+        assert o.view(np.uint32).tolist() == c["o"], c["lanes"]
+    for c in doc["expshift"]:
+        e, s = orc.exp_shift(f32(c["x"]), f32([c["m"]])[0], lanes=c["lanes"])
+        assert e.view(np.uint32).tolist() == c["e"], c["lanes"]
+        assert int(np.float32(s).view(np.uint32)) == c["sum"]
+    n_fused = 0
+    for c in doc["quantize_u8"]:
+        x, inv = f32(c["x"]), f32([c["inv"]])[0]
+        q, s = orc.quantize_row_u8(x, inv, lanes=c["lanes"])
+        assert q.tolist() == c["q"] and s == c["sum"] == sum(c["q"])
+        fused = [i for i in range(len(x)) if round(float(x[i]) * float(inv)) != c["q"][i]]
+        assert fused == c["fused_differs"]
+        n_fused += len(fused)
+    assert n_fused >= 6 * len(doc["quantize_u8"])
+    for c in doc["gelumul"]:
+        o = orc.gelu_mul(f32(c["a"])[None, :], f32(c["b"])[None, :], lanes=c["lanes"])[0]
+        assert o.view(np.uint32).tolist() == c["o"], c["lanes"]
+    assert {c["lanes"] for c in doc["layernorm"]} == {0, 4, 8, 16}
