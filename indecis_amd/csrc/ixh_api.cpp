@@ -937,7 +937,7 @@ int forward(ixh_model *m, const Tuning &tune, const HeadSet *heads, Workspace *w
   }
   if (pooled)
     RUN("pool", 0, dN * 4 * dH + (double)B * 4 * dH,
-        launch_pool(xn, d_offs, B, H, c.pooling == IXH_POOL_CLS && !out.mean, pooled, st));
+        launch_pool(xn, d_offs, B, N, H, c.pooling == IXH_POOL_CLS && !out.mean, pooled, st));
   if (out.zp && heads->rp > 0)
     RUN("head_pooled", 0, (double)B * (4 * dH + 8 * heads->rp),
         launch_head_logits(pooled, B, H, heads->wp.as<double>(), heads->bp.as<float>(), heads->rp, out.zp, st));

@@ -225,8 +225,9 @@ void launch_quant_rows(const float *x, int ld, int M, int K, int8_t *q, int ldq,
 void launch_positions(const int32_t *offs, const int32_t *padoff, int B,
                       int32_t *pos, int32_t *slot, hipStream_t s);
 
-// Mean (float64 accumulation) or first-token pooling, [B][H].
-void launch_pool(const float *xn, const int32_t *offs, int B, int H, int cls,
+// Mean (float64 accumulation) or first-token pooling, [B][H]; N is the
+// batch's token count (it sizes the kernel's ring).
+void launch_pool(const float *xn, const int32_t *offs, int B, int N, int H, int cls,
                  float *out, hipStream_t s);
 
 // head.logits (heads.go:63-74) over T rows.

@@ -537,6 +537,10 @@ __global__ void positions_kernel(const int32_t *offs, const int32_t *padoff, int
 }
 
 // infer.go:265-287: float64 sum over the sequence, in token order.
+// Pooling (infer.go:265-287): the float64 sum of a column over the
+// sequence's tokens in token order, over n, or the first token's row (CLS).
+// Short sequences: one thread a column, its rows loaded 16 ahead of its
+// in-order float64 adds.
 __global__ void pool_kernel(const float *xn, const int32_t *offs, int H, int cls, float *out) {
   const int b = blockIdx.y;
   const int k = blockIdx.x * blockDim.x + threadIdx.x;
@@ -551,7 +555,6 @@ __global__ void pool_kernel(const float *xn, const int32_t *offs, int H, int cls
     *dst = xn[(size_t)o * H + k];
     return;
   }
-  // the float64 sum in token order; rows are loaded 16 ahead of the adds
   double acc = 0.0;
   const float *col = xn + (size_t)o * H + k;
   int t = 0;
@@ -564,6 +567,97 @@ __global__ void pool_kernel(const float *xn, const int32_t *offs, int H, int cls
   }
   for (; t < n; t++) acc += (double)col[(size_t)t * H];
   *dst = (float)(acc / (double)n);
+}
+
+// Long sequences (a batch averaging over 1,024 tokens a sequence): one
+// workgroup of 4 waves per (sequence, 64 columns), wave 0's lane c running
+// column c's chain while all four waves bring the rows in, 64 rows x 64
+// columns (16 KB) a stage by direct-to-LDS buffer loads (4 rows of 256
+// bytes an instruction), 8 stages in a ring and 7 in flight, so that the
+// sequence streams while the chain adds (thread-per-column loads waited on
+// HBM every 16 rows: 362 us for cfg5's 8 x 8,192 tokens). The chain reads
+// the ring with lds_read4, 16 rows ahead of its adds, and adds whole groups
+// of 16 unconditionally (the tail apart), so its only dependence is the
+// float64 add itself.
+constexpr int PL_R = 64, PL_S = 8, PL_STAGE = PL_R * 64 * 4;  // rows a stage, stages, bytes a stage
+__device__ __forceinline__ float lds_read4(uint32_t addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ float lds_read4_now(uint32_t addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ void lgkm_wait16(float (&v)[16]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]),
+                 "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]), "+v"(v[14]),
+                 "+v"(v[15]));
+}
+__global__ __launch_bounds__(256) void pool_ring_kernel(const float *xn, const int32_t *offs, int H, int cls,
+                                                        float *out) {
+  extern __shared__ __attribute__((aligned(16))) float pring[];  // [PL_S][PL_R][64]
+  const int b = blockIdx.y, c0 = 64 * blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int o = offs[b], n = offs[b + 1] - o;
+  const int ncol = min(64, H - c0);
+  float *dst = out + (size_t)b * H + c0 + lane;
+  if (n == 0 || cls) {
+    if (wave == 0 && lane < ncol) *dst = n == 0 ? 0.f : xn[(size_t)o * H + c0 + lane];
+    return;
+  }
+  // rows of the sequence through a descriptor (rows past n read 0, never
+  // added); this thread's 4 loads of a stage: rows 16 wave + 4 k + lane / 16,
+  // columns 4 (lane % 16) .. + 3 (past ncol: read, never added)
+  const __amdgpu_buffer_rsrc_t xr = buf_rsrc(xn + (size_t)o * H + c0, (uint32_t)(n * H * 4));
+  const int ns = (n + PL_R - 1) / PL_R;
+  auto issue = [&](int c) {
+    // past the last stage: an offset past the descriptor's range (no
+    // memory access; the count of loads in flight stays fixed)
+    const int cc = min(c, ns - 1);
+    const uint32_t soff = c < ns ? 0u : 0x80000000u;
+    float *st = pring + (c % PL_S) * (PL_R * 64);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int r = 16 * wave + 4 * k + (lane >> 4);
+      const uint32_t voff = (uint32_t)((PL_R * cc + r) * H + 4 * (lane & 15)) * 4u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(st + 256 * (4 * wave + k)), 16, voff, soff, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < PL_S - 1; c++) issue(c);
+  double acc = 0.0;
+  const uint32_t base = (uint32_t)(size_t)(lds_ptr)pring + 4u * lane;
+  for (int c = 0; c < ns; c++) {
+    wait_vmcnt<4 * (PL_S - 2)>();  // this thread's loads of stage c are in LDS
+    lds_barrier();                 // everyone's are, and stage c - 1 is read
+    issue(c + PL_S - 1);
+    if (wave == 0) {
+      const uint32_t st = base + (uint32_t)((c % PL_S) * PL_STAGE);
+      const int rows = min(PL_R, n - PL_R * c);
+      float v[16], nx[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) v[i] = lds_read4(st + 256u * i);
+      lgkm_wait16(v);
+      int r0 = 0;
+      for (; r0 + 16 <= rows; r0 += 16) {
+        // the next 16 rows' reads in flight while these 16 are added (past
+        // the stage: rows of the ring, not added)
+#pragma unroll
+        for (int i = 0; i < 16; i++) nx[i] = lds_read4(st + 256u * (uint32_t)((r0 + 16 + i) & (PL_R - 1)));
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc += (double)v[i];
+        lgkm_wait16(nx);
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = nx[i];
+      }
+      for (int i = 0; i < rows - r0; i++) acc += (double)lds_read4_now(st + 256u * (uint32_t)(r0 + i));
+    }
+  }
+  wait_vmcnt<0>();  // the loads past the last stage complete before the workgroup ends
+  if (wave == 0 && lane < ncol) *dst = (float)(acc / (double)n);
 }
 
 // head.logits (heads.go:63-74) and the spans head (spans.go:449-459):
@@ -797,11 +891,22 @@ void launch_positions(const int32_t *offs, const int32_t *padoff, int B, int32_t
   positions_kernel<<<B, 256, 0, s>>>(offs, padoff, pos, slot);
 }
 
-void launch_pool(const float *xn, const int32_t *offs, int B, int H, int cls, float *out,
+void launch_pool(const float *xn, const int32_t *offs, int B, int N, int H, int cls, float *out,
                  hipStream_t s) {
   if (B <= 0) return;
-  dim3 grid((H + 255) / 256, B);
-  pool_kernel<<<grid, 256, 0, s>>>(xn, offs, H, cls, out);
+  if (N / B <= 1024) {
+    pool_kernel<<<dim3((H + 255) / 256, B), 256, 0, s>>>(xn, offs, H, cls, out);
+    return;
+  }
+  constexpr int shm = PL_S * PL_STAGE;  // 128 KB
+  static bool attr[64] = {};
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  if (!attr[dev & 63]) {
+    (void)hipFuncSetAttribute((const void *)pool_ring_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, shm);
+    attr[dev & 63] = true;
+  }
+  pool_ring_kernel<<<dim3((H + 63) / 64, B), 256, shm, s>>>(xn, offs, H, cls, out);
 }
 
 void launch_head_logits(const float *x, int T, int H, const double *w, const float *b, int rows,

@@ -44,6 +44,24 @@ def test_cls_pooling():
     gpu.close()
 
 
+@pytest.mark.parametrize("pooling", ["mean", "cls"])
+def test_pool_long_sequences(pooling):
+    """Pooling (infer.go:265-287) on the long-sequence path (a pass whose
+    sequences average over 1,024 tokens: one workgroup per 64 columns
+    streaming the rows through a ring): sequences of 2,000, 1, 0 and 1,300
+    tokens, as one part, mean and CLS, equal the oracle bit for bit."""
+    cfg = small_cfg(layers=1, pooling=pooling)
+    w, gpu, ora = _pair(cfg, seed=49)
+    gpu.set_option("parts", 1)
+    rng = np.random.default_rng(49)
+    seqs = [rng.integers(0, cfg.vocab, size=n, dtype=np.int32) for n in (2000, 1, 0, 1300)]
+    got = gpu.encode_seqs(seqs)
+    want = ora.encode_seqs(seqs)
+    assert f32_bits_equal(got, want), mismatch_report(got, want)
+    assert not got[2].any()
+    gpu.close()
+
+
 def test_panels_upload_equals_rows():
     """ixh_model_set_matrix with IXH_LAYOUT_PANELS (PackedB8.data, int8.go:30)
     gives the model uploaded by rows, bit for bit."""
