@@ -94,10 +94,17 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   const uint32_t bvo = (uint32_t)fr * 32 + 16 * fh;
   const int cb = wave * QC;  // first column of this wave
   v4i bq[PF][NB];
+  // The K loop takes its K steps in a rotated order, the rotation by
+  // workgroup (the int32 sums are exact in any order): the 512 workgroups
+  // that start together then read different weight lines from L2 at a time
+  // instead of all the same ones (189 -> 180 us a launch on cfg4). The
+  // streamed input's ring stays in K order.
+  const int rot = STREAM ? 0 : __builtin_amdgcn_readfirstlane((int)(blockIdx.x % KT));
+  auto phys = [&](int kt) { const int k = kt + rot; return k >= KT ? k - KT : k; };
   auto loadB = [&](int kt, v4i *dst) {
 #pragma unroll
     for (int j = 0; j < NB; j++) {
-      const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)(kt * a.Np + cb + 32 * j) * 32);
+      const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)(phys(kt) * a.Np + cb + 32 * j) * 32);
       dst[j] = __builtin_amdgcn_raw_buffer_load_b128(brs, bvo, so, 0);
     }
   };
@@ -214,7 +221,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   } else {
   const int8_t *pa = panel + fr * Kp;
   auto loadA = [&](int kt) -> v4i {
-    const int c = 2 * kt + fh;
+    const int c = 2 * phys(kt) + fh;
     return *(const v4i *)(pa + 128 * (c >> 3) + 16 * ((c & 7) ^ (fr & 7)));
   };
   v4i fa = loadA(0);
