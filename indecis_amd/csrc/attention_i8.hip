@@ -321,11 +321,14 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   __shared__ __attribute__((aligned(16))) int8_t Ks[CHUNK * KS];
   __shared__ __attribute__((aligned(16))) int8_t Vs[D * VS];
   __shared__ __attribute__((aligned(16))) float kss[CHUNK];
-  // per 32-key group g of the staged chunk: vpre[g][d] = sum of V over the
-  // keys of groups 0..g (int, exact); 40 KB of LDS in all, 4 workgroups per CU
+  // per 32-key group g of the staged chunk: vpre[g][d] = 128 times the sum
+  // of V over the keys of groups 0..g (int, exact: at most 128 * 256 * 127);
+  // 40 KB of LDS in all, 4 workgroups per CU
   __shared__ __attribute__((aligned(16))) int vpre[CHUNK / 32][D];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index as a scalar: the tile loops and the full-tile tests
+  // that derive from it are then scalar branches, not lane masks
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = a.blocks[2 * blockIdx.x], Q0 = a.blocks[2 * blockIdx.x + 1];
   const int h = blockIdx.y;
   const int base = a.offs[b], n = a.offs[b + 1] - base;
@@ -360,6 +363,8 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
     cs_hi = max(cs_hi, __shfl_xor(cs_hi, t));
     ce_lo = min(ce_lo, __shfl_xor(ce_lo, t));
   }
+  cs_hi = __builtin_amdgcn_readfirstlane(cs_hi);  // every lane holds the same value
+  ce_lo = __builtin_amdgcn_readfirstlane(ce_lo);
 
   // key tiles (32 keys) of this wave and of the block
   int wt0, wt1, bk0, bk1;
@@ -431,6 +436,9 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   // after the barrier that follows stage_v: group sums -> prefix sums (the
   // group sums read together, then written: one wait on LDS, not one a
   // group)
+  // global layers: thread d < 64 keeps 128 times the sum of V over the
+  // chunks so far
+  int vtot = 0;
   auto prefix_v = [&] {
     if (tid < D) {
       int gsum[CHUNK / 32];
@@ -438,8 +446,12 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
       for (int g = 0; g < CHUNK / 32; g++) gsum[g] = vpre[g][tid];
 #pragma unroll
       for (int g = 1; g < CHUNK / 32; g++) gsum[g] += gsum[g - 1];
+      if constexpr (GLOBAL) {
+        vtot += 128 * gsum[CHUNK / 32 - 1];  // the chunk's sum (each chunk once)
+      } else {
 #pragma unroll
-      for (int g = 0; g < CHUNK / 32; g++) vpre[g][tid] = gsum[g];
+        for (int g = 0; g < CHUNK / 32; g++) vpre[g][tid] = 128 * gsum[g];
+      }
     }
     __syncthreads();
   };
@@ -520,7 +532,7 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
       prefix_v();
     }
     const int t0 = max(wt0, c0 / 32), t1 = min(wt1, (c0 + CHUNK) / 32);
-    if (t1 > t0) {
+    if (!GLOBAL && t1 > t0) {
       // rows of this lane: dims dt*32 + 8g + 4*(lane/32) + 0..3
 #pragma unroll
       for (int dt = 0; dt < 2; dt++)
@@ -529,10 +541,10 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
           const int d0 = dt * 32 + 8 * g + 4 * (lane >> 5);
           const int4 hi = *(const int4 *)&vpre[t1 - 1 - c0 / 32][d0];
           const int4 lo = t0 > c0 / 32 ? *(const int4 *)&vpre[t0 - 1 - c0 / 32][d0] : int4{0, 0, 0, 0};
-          o[dt][4 * g] += 128 * (hi.x - lo.x);
-          o[dt][4 * g + 1] += 128 * (hi.y - lo.y);
-          o[dt][4 * g + 2] += 128 * (hi.z - lo.z);
-          o[dt][4 * g + 3] += 128 * (hi.w - lo.w);
+          o[dt][4 * g] += hi.x - lo.x;
+          o[dt][4 * g + 1] += hi.y - lo.y;
+          o[dt][4 * g + 2] += hi.z - lo.z;
+          o[dt][4 * g + 3] += hi.w - lo.w;
         }
     }
     for (int t = t0; t < t1; t++) {
@@ -585,6 +597,26 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
         const v4i fv = *(const v4i *)&Vs[(dt * 32 + (lane & 31)) * VS + (t * 32 - c0) + 16 * (lane >> 5)];
         o[dt] = mfma32(fv, bp, o[dt]);
       }
+    }
+  }
+  if constexpr (GLOBAL) {
+    // a wave with queries takes every tile of the sequence, so its
+    // correction is 128 times the sequence's sum of V (keys past it are
+    // zero), added once
+    // (vpre is free: its last reader, the last prefix, passed its barrier)
+    if (tid < D) vpre[0][tid] = vtot;
+    __syncthreads();
+    if (wt1 > wt0) {
+#pragma unroll
+      for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int4 tv = *(const int4 *)&vpre[0][dt * 32 + 8 * g + 4 * (lane >> 5)];
+          o[dt][4 * g] += tv.x;
+          o[dt][4 * g + 1] += tv.y;
+          o[dt][4 * g + 2] += tv.z;
+          o[dt][4 * g + 3] += tv.w;
+        }
     }
   }
   psum += __shfl_xor(psum, 32);
