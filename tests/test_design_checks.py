@@ -47,3 +47,36 @@ def test_attention_tiles_skippable_by_p_zero():
     assert tiles > 2000
     assert skippable * 1000 < tiles
     assert p1 > -6.2344
+
+
+def test_pass1_tile_bound_skips_few():
+    """Attention pass 1 could skip a 32-key tile whose score bound
+    f32(max acc * max ks) lies under the running maximum of every query of
+    the wave (rounding is monotone, so the maximum stays exact). Simulated
+    with Gaussian int8 queries and keys (D 64) and key scales varying by
+    +-20%, tiles in key order as the kernel takes them, 32 queries a wave:
+    about 0% of the tiles qualify at 512 keys, 5% at 2,048 and a third at
+    8,192. The bound needs the tile's integer maximum (the MFMAs still run),
+    so a skipped tile saves the conversion, scaling and maximum (about 40
+    VALU instructions a lane a tile) while the bound and its wave-wide test
+    cost about 12 on every tile: it breaks even near 30%."""
+    rng = np.random.default_rng(7)
+    D, Q = 64, 32
+    share = {}
+    for n in (512, 2048, 8192):
+        q = np.clip(np.rint(rng.standard_normal((Q, D)) * 40), -127, 127).astype(np.int64)
+        k = np.clip(np.rint(rng.standard_normal((n, D)) * 40), -127, 127).astype(np.int64)
+        ks = (rng.uniform(0.8, 1.2, n) * 1e-3).astype(np.float32)
+        acc = q @ k.T  # [Q][n]
+        s = acc.astype(np.float32) * ks[None, :]
+        run = np.full(Q, -np.inf, np.float32)
+        skip = 0
+        for t0 in range(0, n, 32):
+            a = acc[:, t0:t0 + 32].max(axis=1).astype(np.float32)
+            kmax, kmin = ks[t0:t0 + 32].max(), ks[t0:t0 + 32].min()
+            bound = np.where(a >= 0, a * kmax, a * kmin)
+            skip += bool((bound < run).all())
+            run = np.maximum(run, s[:, t0:t0 + 32].max(axis=1))
+        share[n] = skip / (n // 32)
+    print(share)
+    assert share[512] < 0.02 and share[2048] < 0.1 and share[8192] < 0.5
