@@ -41,6 +41,9 @@ WORKLOADS = {
     "cfg4": ("base", 256, 64, 512),
     "cfg3": ("small", 256, 16, 256),
     "cfg5": ("base", 8, 8192, 8192),
+    # not a BASELINE config: cfg4's batch at the reference's own backbone
+    # width (bekko a8m: hidden 384, 6 heads, MLP 2 x 1152; 22 layers as cfg4)
+    "w384": ("bekko", 256, 64, 512),
 }
 
 
@@ -477,6 +480,9 @@ def main():
 
     mname, B, lo, hi = WORKLOADS[args.workload]
     cfg = BASE if mname == "base" else SMALL
+    if mname == "bekko":
+        from indecis_amd.modernbert import Config
+        cfg = Config(hidden=384, layers=22, heads=6, intermediate=1152, vocab=32768)
     weights = Weights.random(cfg, seed=4)
     seqs = make_inputs(np, cfg.vocab, B, lo, hi)
     offs = np.zeros(B + 1, np.int32)

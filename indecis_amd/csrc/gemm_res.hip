@@ -456,8 +456,10 @@ bool launch_ln(const ResArgs &a, int lanes, hipStream_t s) {
 }  // namespace gemm_res_impl
 
 bool gemm_res_supported(int H, int Kp, int Np) {
-  if (Np != H) return false;
-  return (H == 768 && (Kp == 768 || Kp == 1152)) || (H == 256 && (Kp == 256 || Kp == 512));
+  // (weight rows past H, padding of the K-blocked copy, are never read)
+  if (Np < H || Np % 32 != 0) return false;
+  return (H == 768 && (Kp == 768 || Kp == 1152)) || (H == 384 && (Kp == 384 || Kp == 1152)) ||
+         (H == 256 && (Kp == 256 || Kp == 512));
 }
 
 bool launch_gemm_res(const ResArgs &a, int lanes, hipStream_t s) {
@@ -466,6 +468,7 @@ bool launch_gemm_res(const ResArgs &a, int lanes, hipStream_t s) {
   if (!gemm_res_supported(a.H, a.Kp, a.Np) || a.K > a.Kp || a.K % 4 != 0 || a.ldq < a.H) return false;
   if (a.amax && (a.K != a.Kp || a.P <= 0 || a.lda % 4 != 0)) return false;
   if (a.H == 768) return a.Kp == 768 ? launch_ln<24, 6>(a, lanes, s) : launch_ln<36, 6>(a, lanes, s);
+  if (a.H == 384) return a.Kp == 384 ? launch_ln<12, 3>(a, lanes, s) : launch_ln<36, 3>(a, lanes, s);
   return a.Kp == 256 ? launch_ln<8, 2>(a, lanes, s) : launch_ln<16, 2>(a, lanes, s);
 }
 

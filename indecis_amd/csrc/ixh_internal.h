@@ -89,9 +89,9 @@ bool launch_gemm_ws(int epi, const GemmArgs &a, hipStream_t s);
 // The residual GEMMs fused with the quantisation of their input and the
 // LayerNorm + quantisation of their output (gemm_res.hip): X[m][:H] +=
 // deq(quantizeA(A[m][:K]) . B^T), then, with gamma, Q/SA = quantizeA(
-// LayerNorm(X[m], gamma)). Needs Np == H and (H, Kp) one of (768, 768),
-// (768, 1152), (256, 256), (256, 512); returns false (nothing launched)
-// otherwise.
+// LayerNorm(X[m], gamma)). Needs Np >= H (a multiple of 32) and (H, Kp)
+// one of (768, 768), (768, 1152), (384, 384), (384, 1152), (256, 256),
+// (256, 512); returns false (nothing launched) otherwise.
 struct ResArgs {
   const float *A;        // [M][lda] float32 input rows, K valid columns (K % 4 == 0)
   int lda, K, Kp;

@@ -260,7 +260,7 @@ def test_qkv_heads_per_workgroup(nheads):
 
 
 @pytest.mark.parametrize("shape,lanes", [("small", 0), ("small", 4), ("small", 8), ("small", 16),
-                                         ("base", 8), ("base", 16), ("base", 0)])
+                                         ("base", 8), ("base", 16), ("base", 0), ("bekko", 8), ("bekko", 0)])
 def test_fused_residual_gemms(shape, lanes):
     """Option fuse_res: Wo and WoMLP fused with quantizeA of their input rows
     and the next LayerNorm + quantizeA (gemm_res.hip), the input quantised
@@ -270,11 +270,12 @@ def test_fused_residual_gemms(shape, lanes):
     columns), or Wo on the 8-wave whole-row kernel (4, mlp_res.hip), with
     and without the MLP kernel, give the separate kernels' bits (0) and the
     oracle's, for
-    every lane width of the LayerNorm chains, at both model widths, with
-    row counts that leave a partial 32-row block and a last layer without
-    LayerNorm; also with Wi on gemm_i8 (option gemm 1: no GeGLU maxima,
-    so WoMLP takes the panel while Wo streams)."""
-    cfg = small_cfg(layers=3) if shape == "small" else base_cfg(layers=2)
+    every lane width of the LayerNorm chains, at the three model widths
+    (at hidden 384 the 8-wave Wo kernel does not apply: option 4 takes the
+    panel kernel), with row counts that leave a partial 32-row block and a
+    last layer without LayerNorm; also with Wi on gemm_i8 (option gemm 1:
+    no GeGLU maxima, so WoMLP takes the panel while Wo streams)."""
+    cfg = _shape_cfg(shape, 3 if shape == "small" else 2)
     w, gpu, ora = model_pair(cfg, seed=71, lanes=lanes)
     rng = np.random.default_rng(71 + lanes)
     seqs = ids_uniform_lengths(rng, 7, 1, 300, cfg.vocab)
