@@ -237,19 +237,25 @@ __global__ __launch_bounds__(256) void rownorm_kernel(RowArgs a) {
 // the whole row). About 8 KB of LDS per wave instead of the whole rows, so
 // four times as many waves share a CU; the output and quantisation passes
 // run from the registers.
-template <int V, int CPL, int SRC>
+// H = 256*(CPL-1) + 128 (HALF): the last segment is 128 columns, held by
+// lanes 0..31 (the others hold zeros and store nothing).
+template <int V, int CPL, int SRC, bool HALF = false>
 __global__ __launch_bounds__(64) void rownorm_seg_kernel(RowArgs a) {
-  constexpr int RPW = 64 / V, H = 256 * CPL, LD = 256 + V;
+  constexpr int RPW = 64 / V, H = 256 * CPL - (HALF ? 128 : 0), LD = 256 + V;
   __shared__ __attribute__((aligned(16))) float xs[RPW * LD];
   const int lane = threadIdx.x;
   const int grp = blockIdx.x;
+  // this lane's columns of segment c exist (wave-uniform but for the half
+  // segment)
+  auto has = [&](int c) { return !HALF || c < CPL - 1 || lane < 32; };
   float4 x[RPW][CPL];
 #pragma unroll
   for (int r = 0; r < RPW; r++) {
     const int R = min(grp * RPW + r, a.M - 1);  // rows past M repeat the last one
     const RowLoad<SRC> src(a, R);
 #pragma unroll
-    for (int c = 0; c < CPL; c++) x[r][c] = src.load4(4 * (lane + 64 * c));
+    for (int c = 0; c < CPL; c++)
+      x[r][c] = has(c) ? src.load4(4 * (lane + 64 * c)) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   const bool ln = a.gamma != nullptr;
   const int rr = lane / V, l = lane % V;  // this lane's chain: row rr, lane partial l
@@ -257,6 +263,8 @@ __global__ __launch_bounds__(64) void rownorm_seg_kernel(RowArgs a) {
   if (ln) {
     // sum: the chain over segment c continues from segment c-1
     float p = 0.f;
+    // columns of segment c
+    auto segw = [](int c) { return HALF && c == CPL - 1 ? 128 : 256; };
 #pragma unroll
     for (int c = 0; c < CPL; c++) {
 #pragma unroll
@@ -264,7 +272,7 @@ __global__ __launch_bounds__(64) void rownorm_seg_kernel(RowArgs a) {
       __builtin_amdgcn_wave_barrier();
       const float *xr = &xs[rr * LD + l];
 #pragma unroll
-      for (int k = 0; k < 256 / V; k++) p = p + xr[V * k];
+      for (int k = 0; k < segw(c) / V; k++) p = p + xr[V * k];
       __builtin_amdgcn_wave_barrier();
     }
     double sum = 0.0;  // lanes in order, in float64 (vec_simd.go:294-297)
@@ -279,7 +287,7 @@ __global__ __launch_bounds__(64) void rownorm_seg_kernel(RowArgs a) {
       __builtin_amdgcn_wave_barrier();
       const float *xr = &xs[rr * LD + l];
 #pragma unroll
-      for (int k = 0; k < 256 / V; k++) {
+      for (int k = 0; k < segw(c) / V; k++) {
         const float d = xr[V * k] - mean;
         q = __builtin_fmaf(d, d, q);
       }
@@ -299,6 +307,7 @@ __global__ __launch_bounds__(64) void rownorm_seg_kernel(RowArgs a) {
     mx[r] = 0.f;
 #pragma unroll
     for (int c = 0; c < CPL; c++) {
+      if (!has(c)) continue;
       float4 v = x[r][c];
       if (ln) {
         const float4 g = *(const float4 *)&a.gamma[4 * (lane + 64 * c)];
@@ -329,6 +338,7 @@ __global__ __launch_bounds__(64) void rownorm_seg_kernel(RowArgs a) {
     }
 #pragma unroll
     for (int c = 0; c < CPL; c++) {
+      if (!has(c)) continue;
       const float4 v = x[r][c];
       const int q0 = q8(v.x, inv), q1 = q8(v.y, inv), q2 = q8(v.z, inv), q3 = q8(v.w, inv);
       *(int *)qbyte(a, R, 4 * (lane + 64 * c)) = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (q3 << 24);
@@ -829,6 +839,21 @@ void launch_resident(Kern kern, int work, int threads, const RowArgs &a, hipStre
 void launch_rownorm(const RowArgs &a, hipStream_t s) {
   if (a.M <= 0) return;
   const int src = !a.ids ? 0 : a.emb_format == 0 ? 1 : a.emb_format == 1 ? 2 : 3;
+  if ((a.lanes == 8 || a.lanes == 16) && a.H == 384 && a.seg != 0) {
+    // a 256-column segment and a 128-column one
+    const int rpw = 64 / a.lanes, groups = (a.M + rpw - 1) / rpw;
+#define IXH_SEGH(VV)                                                                        \
+  if (a.lanes == VV) {                                                                      \
+    switch (src) {                                                                          \
+    case 0: rownorm_seg_kernel<VV, 2, 0, true><<<groups, 64, 0, s>>>(a); return;           \
+    case 1: rownorm_seg_kernel<VV, 2, 1, true><<<groups, 64, 0, s>>>(a); return;           \
+    case 2: rownorm_seg_kernel<VV, 2, 2, true><<<groups, 64, 0, s>>>(a); return;           \
+    default: rownorm_seg_kernel<VV, 2, 3, true><<<groups, 64, 0, s>>>(a); return;          \
+    }                                                                                       \
+  }
+    IXH_SEGH(8) IXH_SEGH(16)
+#undef IXH_SEGH
+  }
   if (a.lanes > 0 && a.H % 256 == 0 && a.H <= 1024 && !(a.lanes == 4 && a.H > 768)) {
     const int V = a.lanes, cpl = a.H / 256, rpw = 64 / V;
     const int groups = (a.M + rpw - 1) / rpw;

@@ -359,22 +359,24 @@ def test_deq_bound_fallback(which):
         gpu.close()
 
 
-def test_bekko_width_exact():
+@pytest.mark.parametrize("lanes", [8, 16])
+def test_bekko_width_exact(lanes):
     """The reference's own backbone width (bekko a8m: hidden 384, 6 heads,
     MLP 2 x 1152; linalg/gemm_test.go:104-105) through the whole encoder,
-    with the fused kernels on (the 64-row MLP kernel, the fused QKV
-    kernel) and off, pooled and per token, against the oracle."""
+    with the fused kernels on (the 64-row MLP kernel, the fused QKV and
+    residual kernels, the LayerNorm segment kernel with a 128-column
+    segment) and off, pooled and per token, against the oracle."""
     cfg = bekko_cfg(layers=3)
-    w, gpu, ora = model_pair(cfg, seed=83, lanes=8)
+    w, gpu, ora = model_pair(cfg, seed=83, lanes=lanes)
     rng = np.random.default_rng(83)
     seqs = ids_uniform_lengths(rng, 12, 1, 400, cfg.vocab)
     want, _ = ora.encode_tokens(seqs)
-    for mlp, res, qkv in ((2, 1, 1), (0, 0, 0), (2, 0, 0), (1, 1, 1)):
-        with options(gpu, fuse_mlp=mlp, fuse_res=res, qkv_fused=qkv):
+    for mlp, res, qkv, seg in ((2, 1, 1, 1), (0, 0, 0, 1), (2, 0, 0, 1), (1, 1, 1, 1), (2, 1, 1, 0)):
+        with options(gpu, fuse_mlp=mlp, fuse_res=res, qkv_fused=qkv, ln_seg=seg):
             got = gpu.encode_tokens(seqs)
             pooled = gpu.encode_seqs(seqs)
-        assert f32_bits_equal(got, want), ((mlp, res, qkv), mismatch_report(got, want))
-        assert f32_bits_equal(pooled, ora.encode_seqs(seqs)), (mlp, res, qkv)
+        assert f32_bits_equal(got, want), ((mlp, res, qkv, seg), mismatch_report(got, want))
+        assert f32_bits_equal(pooled, ora.encode_seqs(seqs)), (mlp, res, qkv, seg)
 
 
 @pytest.mark.parametrize("shape", ["small", "base"])

@@ -100,7 +100,7 @@ def test_matmul8_rows_independent():
 
 
 @pytest.mark.parametrize("lanes", [0, 4, 8, 16])
-@pytest.mark.parametrize("m,h", [(1, 4), (7, 36), (64, 256), (300, 768), (5, 1152)])
+@pytest.mark.parametrize("m,h", [(1, 4), (7, 36), (64, 256), (33, 384), (300, 768), (5, 1152)])
 def test_layernorm_quant_exact(m, h, lanes):
     rng = np.random.default_rng(m * h + lanes)
     x = (rng.standard_normal((m, h)) * 3 + 0.5).astype(np.float32)
