@@ -10,8 +10,8 @@ weights of the ModernBERT-base shape (H 768, 22 layers, 12 heads, GeGLU
 pooled [256, 768] output stays there (ixh_encode_device).
 
 A large batch runs as token-balanced parts on several streams (the
-library's default: three for cfg4), so kernels of the parts overlap; `value` and
-`ms_per_step` are measured that way. `roofline` is for the kernel class with
+library's default: two from 4,096 tokens on), so kernels of the parts
+overlap; `value` and `ms_per_step` are measured that way. `roofline` is for the kernel class with
 the most GPU time in one untimed pass of the batch as one part; it is
 measured over K further timed steps with the batch as one part (the kernel
 running alone), with that class's launches (only) bracketed by timing-only
