@@ -603,6 +603,11 @@ def main():
     gemm_ops = sum(st["ops"] for st in gemm)
     gemm_ms = sum(st["ms"] for st in gemm)
 
+    # the device's own int8 MFMA rate (every wave issuing MFMAs from
+    # registers): the scale the kernels' fractions of the dense peak sit on
+    from indecis_amd import linalg
+    loop_rate = linalg.check_mfma_rate(0)
+
     cpu = None
     if args.cpu_tokens > 0:
         cpu = cpu_baseline(np, weights, seqs, args.cpu_tokens)
@@ -630,6 +635,9 @@ def main():
         "gemm_mfma_frac": round(gemm_ops / (gemm_ms / 1e3) / PEAK_INT8_OPS, 4) if gemm_ms else None,
         "roofline": roof,
         "roofline_concurrent": roof_conc,
+        "mfma_loop": {"TOP/s": round(loop_rate / 1e12, 1), "frac": round(loop_rate / PEAK_INT8_OPS, 4),
+                      "note": "int8 MFMAs issued back to back from registers by four waves a SIMD "
+                              "(ixh_check_mfma_rate), after the timed region"},
         "cpu_baseline": cpu,
         "kernels": kernels,
         "kernels_note": "per kernel class, from one untimed pass with every launch timed by HIP events",

@@ -400,6 +400,13 @@ int ixh_check_exp255(int device, int64_t bad[2], float max_err[2], int64_t *unde
  * the FMA form, bad[1] for the scalar form; both must be 0. */
 int ixh_check_gelu(int device, int64_t bad[2]);
 
+/* Rate check of the int8 matrix cores (no counterpart in the reference; the
+ * scale of the roofline figures): every wave of four a SIMD issues
+ * 4 * iters v_mfma_i32_32x32x32_i8 back to back from registers (iters in
+ * 1 .. 2^22). *ops_per_s: int8 operations (two a multiply-add) a second
+ * over the timed launch, to set against the 5.0e15 dense peak. */
+int ixh_check_mfma_rate(int device, int iters, double *ops_per_s);
+
 #ifdef __cplusplus
 }
 #endif

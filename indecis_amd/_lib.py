@@ -24,7 +24,7 @@ EXPORTS = [
     "ixh_embed_texts", "ixh_embed_normalize",
     "ixh_matmul8_tile", "ixh_layernorm_quant", "ixh_ln_matmul8_geglu", "ixh_attend8",
     "ixh_model_set_profiling", "ixh_model_set_profile_filter", "ixh_model_profile",
-    "ixh_check_exp255", "ixh_check_gelu", "ixh_batcher_create", "ixh_batcher_encode", "ixh_batcher_stats",
+    "ixh_check_exp255", "ixh_check_gelu", "ixh_check_mfma_rate", "ixh_batcher_create", "ixh_batcher_encode", "ixh_batcher_stats",
     "ixh_batcher_destroy", "ixh_model_set_option", "ixh_model_get_option", "ixh_packb8_set_option",
     "ixh_model_set_heads", "ixh_encode_heads", "ixh_matmul8_noalloc",
 ]
@@ -119,6 +119,7 @@ def lib():
         "ixh_check_exp255": [C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_float),
                              C.POINTER(C.c_int64)],
         "ixh_check_gelu": [C.c_int, C.POINTER(C.c_int64)],
+        "ixh_check_mfma_rate": [C.c_int, C.c_int, C.POINTER(C.c_double)],
         "ixh_batcher_create": [vp, C.c_int, C.c_int, C.POINTER(vp)],
         "ixh_batcher_encode": [vp, vp, vp, C.c_int, vp],
         "ixh_batcher_stats": [vp, C.POINTER(C.c_int64), C.POINTER(C.c_int64)],

@@ -360,4 +360,28 @@ void launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
   }
 }
 
+// The int8 MFMA issue rate: every wave of the grid runs `iters` rounds of
+// four independent v_mfma_i32_32x32x32_i8 from registers (no memory in the
+// loop), then stores a checksum of its accumulators (so that the loop is
+// kept).
+__global__ __launch_bounds__(256) void mfma_rate_kernel(int iters, int *out) {
+  const int t = threadIdx.x;
+  const v4i a = {t, 3 * t + 1, 5 * t + 2, 7 * t + 3}, b = {11 * t, 13 * t + 1, 17 * t + 2, 19 * t + 3};
+  v16i c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  for (int i = 0; i < iters; i++) {
+    c0 = mfma32(a, b, c0);
+    c1 = mfma32(b, a, c1);
+    c2 = mfma32(a, a, c2);
+    c3 = mfma32(b, b, c3);
+  }
+  int sum = 0;
+#pragma unroll
+  for (int r = 0; r < 16; r++) sum += c0[r] ^ c1[r] ^ c2[r] ^ c3[r];
+  out[(size_t)blockIdx.x * 256 + t] = sum;
+}
+
+void launch_mfma_rate(int blocks, int iters, int *out, hipStream_t s) {
+  mfma_rate_kernel<<<blocks, 256, 0, s>>>(iters, out);
+}
+
 }  // namespace ixh

@@ -2151,6 +2151,41 @@ int ixh_check_gelu(int device, int64_t bad[2]) {
   return IXH_OK;
 }
 
+int ixh_check_mfma_rate(int device, int iters, double *ops_per_s) {
+  if (!ops_per_s || iters < 1 || iters > (1 << 22)) return fail(IXH_EINVAL, "linalg: hip: bad MFMA rate check");
+  DEVGUARD(device);
+  TmpStream ts;
+  HIPCK(hipStreamCreateWithFlags(&ts.s, hipStreamNonBlocking));
+  // four workgroups of four waves a CU: four waves a SIMD
+  const int blocks = 4 * device_cus();
+  DevBuf dout;
+  int rc;
+  if ((rc = dout.ensure((size_t)blocks * 256 * sizeof(int)))) return rc;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  HIPCK(hipEventCreate(&e0));
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return fail(IXH_EHIP, "linalg: hip: event");
+  }
+  launch_mfma_rate(blocks, iters, dout.as<int>(), ts.s);  // warm-up
+  hipError_t e = hipEventRecord(e0, ts.s);
+  if (e == hipSuccess) {
+    launch_mfma_rate(blocks, iters, dout.as<int>(), ts.s);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipEventRecord(e1, ts.s);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (e != hipSuccess) return fail(IXH_EHIP, "linalg: hip: %s (MFMA rate check)", hipGetErrorString(e));
+  // 32 x 32 x 32 multiply-adds = 65,536 operations an MFMA
+  const double ops = (double)blocks * 4 * 4 * (double)iters * 65536.0;
+  *ops_per_s = ms > 0.f ? ops / (ms * 1e-3) : 0.0;
+  return IXH_OK;
+}
+
 }  // extern "C"
 
 // ---- batching of concurrent requests ----------------------------------------

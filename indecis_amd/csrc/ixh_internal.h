@@ -267,6 +267,9 @@ void launch_attn_main(const AttnArgs &a, hipStream_t s);
 // max err scalar bits, undecided}
 void launch_check_exp255(uint32_t lo, uint32_t hi, unsigned long long *res, hipStream_t s);
 void launch_check_gelu(unsigned long long *res, hipStream_t s);
+// blocks workgroups of 4 waves, each wave 4 * iters int8 MFMAs 32x32x32;
+// out: blocks * 256 ints (checksums)
+void launch_mfma_rate(int blocks, int iters, int *out, hipStream_t s);
 
 constexpr int kAttnQBlock = 128;  // queries per workgroup (4 waves x 32)
 constexpr int kKeyPad = 64;       // key slots of a sequence are padded to this

@@ -148,6 +148,14 @@ def check_exp255(device=0):
     return int(bad[0]), int(bad[1]), float(err[0]), float(err[1]), int(und.value)
 
 
+def check_mfma_rate(device=0, iters=20000):
+    """int8 operations a second that the device's matrix cores sustain when
+    every wave issues v_mfma_i32_32x32x32_i8 back to back from registers."""
+    r = C.c_double()
+    _lib.check(_lib.lib().ixh_check_mfma_rate(device, iters, C.byref(r)))
+    return float(r.value)
+
+
 def check_gelu(device=0):
     """Runs the device self-check of the GELU's division and clamp over
     every float input: returns (bad_fma_form, bad_scalar_form); both must

@@ -317,3 +317,10 @@ def test_gelu_division_every_float():
     result in every bit."""
     bad_fma, bad_scalar = linalg.check_gelu()
     assert bad_fma == 0 and bad_scalar == 0, (bad_fma, bad_scalar)
+
+
+def test_mfma_rate_check():
+    """ixh_check_mfma_rate: int8 MFMAs issued back to back from registers
+    run at a sizeable fraction of the 5.0e15 dense peak, never above it."""
+    r = linalg.check_mfma_rate(0, iters=20000)
+    assert 0.2 * 5.0e15 < r < 1.05 * 5.0e15, r
