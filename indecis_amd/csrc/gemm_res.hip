@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
 #pragma unroll
       for (int c = 0; c < CPL; c++) {
         const int i = 4 * (lane + 64 * c);
-        v[u][c] = i < a.K ? *(const float4 *)(src + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[u][c] = i < a.K ? load_stream_f4(src + i) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
 #pragma unroll
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   for (int j = 0; j < NB; j++) {
     const uint32_t vo = (uint32_t)(4 * fh * H + cb + 32 * j + fr) * 4;
 #pragma unroll
-    for (int r = 0; r < 16; r++) x[j][r] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(xrs, vo, roff(r), 0));
+    for (int r = 0; r < 16; r++) x[j][r] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(xrs, vo, roff(r), kStreamPolicy));
   }
   // (with the weights' bound, checked on upload, f32(acc + 128 colsum) -
   // zc is f32(acc) exactly)
@@ -263,14 +263,14 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
       for (int r = 0; r < 16; r++) {
         const float v = ((float)acc[j][r] * sb) * sa_s[acc_row(r, lane)];
         x[j][r] = x[j][r] + v;
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x[j][r]), xrs, vo, roff(r), 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x[j][r]), xrs, vo, roff(r), kStreamPolicy);
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const float v = deq(acc[j][r] + c1, zc, sb, sa_s[acc_row(r, lane)]);
         x[j][r] = x[j][r] + v;
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x[j][r]), xrs, vo, roff(r), 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x[j][r]), xrs, vo, roff(r), kStreamPolicy);
       }
     }
   }
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(256, 2) void gemm_res_kernel(ResArgs a) {
   constexpr int C16 = H / 16;  // 16-byte pieces of a row
   for (int idx = tid; idx < BM * C16; idx += 256) {
     const int row = idx / C16, c = idx - row * C16;
-    if (m0 + row < M) *(v4i *)(a.Q + (size_t)(m0 + row) * a.ldq + 16 * c) = *(const v4i *)(qs + row * H + 16 * c);
+    if (m0 + row < M) store_stream_16(a.Q + (size_t)(m0 + row) * a.ldq + 16 * c, *(const v4i *)(qs + row * H + 16 * c));
   }
   for (int idx = tid; idx < BM * (a.ldq - H); idx += 256) {
     const int row = idx / (a.ldq - H), c = H + idx - row * (a.ldq - H);

@@ -166,7 +166,7 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
 #pragma unroll
     for (int u = 0; u < BM * PCS / 512; u++) {
       const int idx = tid + 512 * u, tok = idx / PCS, p = idx - tok * PCS;
-      v[u] = __builtin_amdgcn_raw_buffer_load_b128(ars, (uint32_t)(tok * a.ldq + 16 * p), 0, 0);
+      v[u] = __builtin_amdgcn_raw_buffer_load_b128(ars, (uint32_t)(tok * a.ldq + 16 * p), 0, kStreamPolicy);
     }
 #pragma unroll
     for (int u = 0; u < BM * PCS / 512; u++) {
@@ -377,7 +377,8 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
   auto load_stage = [&](int s, v4i *dst) {
 #pragma unroll
     for (int u = 0; u < 8; u++)
-      dst[u] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (uint32_t)(((8 * wave + u) * H + SWC * s + 4 * lane) * 4), 0, 0);
+      dst[u] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (uint32_t)(((8 * wave + u) * H + SWC * s + 4 * lane) * 4), 0,
+                                                     kStreamPolicy);
   };
   v4i xin[NJ > 1 ? 2 : 1][8];
   load_stage(0, xin[0]);
@@ -548,7 +549,8 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
     for (int u = 0; u < 8; u++)
       if (4 * lane < scw)
         __builtin_amdgcn_raw_buffer_store_b128(*(const v4i *)(xb + (8 * wave + u) * XST + 4 * lane), xrs,
-                                               (uint32_t)(((8 * wave + u) * H + SWC * s + 4 * lane) * 4), 0, 0);
+                                               (uint32_t)(((8 * wave + u) * H + SWC * s + 4 * lane) * 4), 0,
+                                               kStreamPolicy);
     if constexpr (LN) chains(s, 0);
   });
   if constexpr (!LN) return;
@@ -629,9 +631,9 @@ __global__ __launch_bounds__(512, 1) void mlp_block_kernel(MlpArgs a) {
       for (int q = 0; q < 4; q++) pk[q] = pack4(x[j][b][4 * q], x[j][b][4 * q + 1], x[j][b][4 * q + 2], x[j][b][4 * q + 3], inv);
       if (tok < rows) {
         if (a.Qk)  // K-blocked: 32-byte block c of row m0 + tok at (c * qk_rows + m0 + tok) * 32
-          *(v4i *)(a.Qk + ((size_t)c * a.qk_rows + m0 + tok) * 32 + 16 * fh) = pk;
+          store_stream_16(a.Qk + ((size_t)c * a.qk_rows + m0 + tok) * 32 + 16 * fh, pk);
         else
-          *(v4i *)(a.Q + (size_t)(m0 + tok) * ldq + 32 * c + 16 * fh) = pk;
+          store_stream_16(a.Q + (size_t)(m0 + tok) * ldq + 32 * c + 16 * fh, pk);
       }
     }
   }
