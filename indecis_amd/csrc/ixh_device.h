@@ -88,7 +88,7 @@ __device__ __forceinline__ float exp32_simd(float v) {
 // accesses whose wave instruction covers whole 128-byte lines: on stores
 // of 16 bytes a row (the QKV kernel's K and Q rows, attention's context)
 // the hint made those kernels 6% and 12% slower; on the final LayerNorm's
-// output, which pooling reads next, 76 -> 87 µs.
+// output, which pooling reads next, 76 -> 87 us.
 constexpr int kStreamPolicy = 2;
 typedef float f4v __attribute__((ext_vector_type(4)));
 // a float4 of streamed data through a plain pointer (global_load ... nt)
