@@ -304,7 +304,10 @@ __global__ __launch_bounds__(256, MI == 4 ? 2 : 3) void gemm_i8_kernel(GemmArgs 
           if (vec && col + 4 <= a.n_valid) {
             if (acc_in)
               v = make_float4(old[u].x + v.x, old[u].y + v.y, old[u].z + v.z, old[u].w + v.w);
-            *(float4 *)dst = v;
+            if constexpr (EPI == EPI_ROPE)  // float32 K and V: 256 bytes of a row a quarter-wave, read by the next kernels once
+              store_stream_16(dst, v4i{__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z), __float_as_int(v.w)});
+            else
+              *(float4 *)dst = v;
           } else {
             const float e[4] = {v.x, v.y, v.z, v.w};
             for (int t = 0; t < 4; t++)
