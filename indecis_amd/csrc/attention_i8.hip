@@ -189,7 +189,7 @@ __global__ __launch_bounds__(512, 4) void attn_prologue_rows_kernel(AttnArgs a) 
 #pragma unroll
     for (int u = 0; u < 16; u++) {
       const int j = rg + 32 * u;
-      kr[u] = j < n ? buf_load_f4(rows, voff, (uint32_t)(32 * u) * ld * 4) : zero4;
+      kr[u] = j < n ? buf_load_f4<kStreamPolicy>(rows, voff, (uint32_t)(32 * u) * ld * 4) : zero4;
     }
     // sum of K in key order (AddTo, attention8.go:224-228)
     float ksum = 0.f;
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(512, 4) void attn_prologue_rows_kernel(AttnArgs a) 
 #pragma unroll
     for (int u = 0; u < 16; u++) {
       const int j = 16 * rg + u;
-      vr[u] = j < n ? buf_load_f4(rows, voff, (uint32_t)u * ld * 4) : zero4;
+      vr[u] = j < n ? buf_load_f4<kStreamPolicy>(rows, voff, (uint32_t)u * ld * 4) : zero4;
     }
     if (PART) {
       if (tid < D) mean[tid] = stat[D + tid];

@@ -104,8 +104,9 @@ __device__ __forceinline__ void store_stream_16(void *p, v4i v) { __builtin_nont
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
 }
+template <int POLICY = 0>
 __device__ __forceinline__ float4 buf_load_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  const v4i t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  const v4i t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POLICY);
   return make_float4(__int_as_float(t[0]), __int_as_float(t[1]), __int_as_float(t[2]),
                      __int_as_float(t[3]));
 }
