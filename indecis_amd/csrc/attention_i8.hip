@@ -329,8 +329,15 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
   // the wave index as a scalar: the tile loops and the full-tile tests
   // that derive from it are then scalar branches, not lane masks
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int b = a.blocks[2 * blockIdx.x], Q0 = a.blocks[2 * blockIdx.x + 1];
-  const int h = blockIdx.y;
+  // work item j = head * nblocks + entry (a sequence's query blocks are
+  // consecutive entries). Workgroup L runs on XCD L % 8; each XCD takes a
+  // contiguous run of items, so the query blocks of one (sequence, head)
+  // run on one XCD and share its K and V in that XCD's L2.
+  const int per = (a.nblocks * a.nh + 7) / 8;
+  const int j = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (j >= a.nblocks * a.nh) return;  // the whole workgroup
+  const int h = j / a.nblocks, ent = j - h * a.nblocks;
+  const int b = a.blocks[2 * ent], Q0 = a.blocks[2 * ent + 1];
   const int base = a.offs[b], n = a.offs[b + 1] - base;
   const int slot0 = a.padoff[b];
   const int npad = (n + kKeyPad - 1) / kKeyPad * kKeyPad;
@@ -724,7 +731,8 @@ void launch_attn_prologue(const AttnArgs &a, hipStream_t s) {
 
 void launch_attn_main(const AttnArgs &a, hipStream_t s) {
   if (a.nblocks <= 0) return;
-  dim3 grid(a.nblocks, a.nh);
+  // 8 runs of (nblocks * nh + 7) / 8 items, one an XCD (see the kernel)
+  const dim3 grid(8 * ((a.nblocks * a.nh + 7) / 8));
   if (a.window < 0)
     attn_main_kernel<true><<<grid, 256, 0, s>>>(a);
   else
