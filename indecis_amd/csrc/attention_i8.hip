@@ -627,10 +627,16 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
     }
   }
   psum += __shfl_xor(psum, 32);
-  if (!qact) return;
-  const float sp = 1.0f / (float)(int)psum;
+  // The context rows leave through LDS: each wave stages its 32 queries x
+  // 64 dimensions in the free K or V staging area, then stores whole
+  // 256-byte row pieces (16 lanes a query), non-temporal (the Wo kernel
+  // reads them once).
+  constexpr int OLD = D + 4;  // floats a staged row (conflict-free writes)
+  static_assert(2 * 32 * OLD * 4 <= CHUNK * KS && 2 * 32 * OLD * 4 <= D * VS, "context staging");
+  __syncthreads();  // every wave is past pass 2: Ks and Vs are free
+  float *stg = (float *)(wave < 2 ? Ks : Vs) + (wave & 1) * (32 * OLD);
+  const float sp = qact ? 1.0f / (float)(int)psum : 0.f;
   const float *vsd = a.vs + ((size_t)b * a.nh + h) * D;
-  float *orow = a.ctx + (size_t)(base + qi) * H + h * D;
   float mx = 0.f;  // max |ctx| of this (row, head), for the fused Wo GEMM
   // the V scales of this lane's 32 dimensions, every load issued before
   // the first store (the compiler cannot tell vs from ctx)
@@ -654,10 +660,21 @@ __global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs
         ov[u] = (((float)tile - 0.0f) * vv[u]) * sp;
         mx = __builtin_fmaxf(mx, fabsf(ov[u]));
       }
-      *(float4 *)(orow + d0) = make_float4(ov[0], ov[1], ov[2], ov[3]);
+      *(float4 *)(stg + (lane & 31) * OLD + d0) = make_float4(ov[0], ov[1], ov[2], ov[3]);
     }
   }
-  if (a.rmax) {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt 0: this wave's staging writes are done
+  __builtin_amdgcn_wave_barrier();
+  // query 4u + lane/16 of the wave, dimensions 4 (lane % 16) .. + 3
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    const int ql = 4 * u + (lane >> 4), qg = q0 + ql;
+    const float4 v = *(const float4 *)(stg + ql * OLD + 4 * (lane & 15));
+    if (qg < n)
+      store_stream_16(a.ctx + (size_t)(base + qg) * H + h * D + 4 * (lane & 15),
+                      v4i{__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z), __float_as_int(v.w)});
+  }
+  if (a.rmax && qact) {
     mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));  // the other 32 dimensions
     if (lane < 32) a.rmax[(size_t)(base + qi) * a.nh + h] = mx;
   }
