@@ -4,7 +4,7 @@
  * This is the drop-in boundary for indecis's int8 encoder forward pass:
  * the body of internal/modernbert.(*Model).run (infer.go:304-430) and the
  * linalg entry points it calls. A cgo file built under the `rocm` tag
- * binds these functions (see INTEGRATION.md); EncodeSeqs, EncodeTokens and
+ * binds these functions; EncodeSeqs, EncodeTokens and
  * Encode keep their Go signatures, so model.go:425, batch.go:71,
  * spans.go:423, distill.go:121 and open.go:131 switch with no change.
  *

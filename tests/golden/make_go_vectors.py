@@ -5,7 +5,7 @@ LayerNormRow (linalg/vec_simd.go:285-327, vec_scalar.go:66-81), ExpShift
 (vec_simd.go:64-91, vec_scalar.go:23-31) and GeluMul (vec_simd.go:125-160,
 gelu_amd64.s) — for every Go simd lane width V (0: a build without
 GOEXPERIMENT=simd; 4, 8, 16). A maintainer with Go runs the reference on
-the same inputs (the Go test in INTEGRATION.md) and compares bit for bit.
+the same inputs (a Go test that reads this file) and compares bit for bit.
 
 The oracle restates the Go source with scalar code unfused (GOAMD64 v1/v2).
 The QuantizeRowU8 rows end in crafted values where f32(x*inv) is exactly a

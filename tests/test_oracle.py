@@ -776,7 +776,8 @@ def test_go_semantics_vectors():
     """tests/golden/go_semantics.json (written by make_go_vectors.py): the
     oracle still gives, bit for bit, the LayerNormRow, ExpShift,
     QuantizeRowU8 and GeluMul outputs that a maintainer compares the Go
-    reference against, for every lane width; and each
+    reference against (with a Go test over the same file), for every lane
+    width; and each
     crafted QuantizeRowU8 tie is one where a fused x*inv + magic (RNE of the
     exact product, computed here in float64) rounds the other way, so the
     vectors tell a build that fuses the tail."""
