@@ -316,8 +316,12 @@ __global__ __launch_bounds__(256) void attn_quant_q_kernel(AttnArgs a) {
   if (sub == 0) a.sq[(size_t)row * a.nh + h] = s * a.scale;
 }
 
+// Four waves a SIMD (at most 128 VGPRs) for both layer kinds: the local
+// kernel then spills 8 values, stored once in the prologue and reloaded once
+// a chunk and in the epilogue, never in the tile loops; 117-122 against
+// 129-131 us a launch at three waves a SIMD (139 VGPRs) on cfg4.
 template <bool GLOBAL>
-__global__ __launch_bounds__(256, GLOBAL ? 4 : 3) void attn_main_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 4) void attn_main_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t Ks[CHUNK * KS];
   __shared__ __attribute__((aligned(16))) int8_t Vs[D * VS];
   __shared__ __attribute__((aligned(16))) float kss[CHUNK];
