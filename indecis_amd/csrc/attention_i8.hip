@@ -316,10 +316,8 @@ __global__ __launch_bounds__(256) void attn_quant_q_kernel(AttnArgs a) {
   if (sub == 0) a.sq[(size_t)row * a.nh + h] = s * a.scale;
 }
 
-// Four waves a SIMD (at most 128 VGPRs) for both layer kinds: the local
-// kernel then spills 8 values, stored once in the prologue and reloaded once
-// a chunk and in the epilogue, never in the tile loops; 117-122 against
-// 129-131 us a launch at three waves a SIMD (139 VGPRs) on cfg4.
+// Four waves a SIMD (at most 128 VGPRs) for both layer kinds: local layers
+// 116-118 us a launch on cfg4 against 129-131 at three waves a SIMD.
 template <bool GLOBAL>
 __global__ __launch_bounds__(256, 4) void attn_main_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t Ks[CHUNK * KS];
@@ -412,6 +410,12 @@ __global__ __launch_bounds__(256, 4) void attn_main_kernel(AttnArgs a) {
   const auto ksrs = buf_rsrc(ksglob, (uint32_t)npad * 4);
   const auto vrs = buf_rsrc(vglob, (uint32_t)((D - 1) * a.Npad + npad));
   auto stage = [&](int c0, bool with_v) {
+    // local layers: the thread's offsets are recomputed at each call from
+    // an opaque copy of its index, instead of being kept in VGPRs across
+    // the score loops between calls (held to 128 VGPRs, the kernel spilled
+    // 8 of them: 8 KB a workgroup written to scratch)
+    int tid = threadIdx.x;
+    if constexpr (!GLOBAL) asm volatile("" : "+v"(tid));
     v4i kw[NKP], vlo[NVG], vhi[NVG];
 #pragma unroll
     for (int i = 0; i < NKP; i++)
