@@ -129,6 +129,24 @@ def test_attend8_exact(n, window, lanes):
     assert f32_bits_equal(o, ref), mismatch_report(o, ref)
 
 
+@pytest.mark.parametrize("lanes", [8, 0])
+@pytest.mark.parametrize("window", [100, 300])
+@pytest.mark.parametrize("n", [300, 1025])
+def test_attend8_wide_window_exact(n, window, lanes):
+    """Sliding windows wider than 64 keys a side: a workgroup's 128 queries
+    then need more than one staged chunk of 256 keys, so pass 2 stages K
+    and V again chunk by chunk (a path the encoder's window of 64 keys a
+    side never takes). Bit for bit against the oracle."""
+    rng = np.random.default_rng(n * 100 + window + 7 * lanes + 1)
+    D = 64
+    q = (rng.standard_normal((n, D)) * 2).astype(np.float32)
+    k = (rng.standard_normal((n, D)) * 2).astype(np.float32) + (np.arange(n * D) % D % 7).reshape(n, D).astype(np.float32)
+    v = rng.standard_normal((n, D)).astype(np.float32)
+    ref = orc.attend8(q, k, v, window, 0.125, lanes)
+    o = linalg.attend8(q, k, v, window, 0.125, lanes)
+    assert f32_bits_equal(o, ref), mismatch_report(o, ref)
+
+
 @pytest.mark.parametrize("tile_cfg", [0, 1, 2])
 def test_gemm_tile_configs(tile_cfg):
     """The gemm_i8 kernel alone (option gemm 1) in its default 128x128 and
